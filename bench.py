@@ -1,0 +1,223 @@
+#!/usr/bin/env python3
+"""Benchmark of the routed-expert SwiGLU FFN on one MI355X.
+
+Default workload (the config the metric is quoted
+on): a Mixtral-8x7B-shaped MoE stack, 32 layers x 8 Q4_0 experts
+(d_model 4096, d_ff 14336; 256 experts = 25.4 GB resident in HBM), top-2
+routing from N(0,1) logits per token per layer (softmax, top-2,
+renormalised), decode batch 1.  One step = one token through all 32 layers:
+layer l reads its own N(0,1) input vector x_l (standing in for the normed
+residual stream, which keeps magnitudes bounded without a norm kernel) and
+accumulates out += sum_i w_i y_i (the engine's WeightedInto accumulate).  Weights are synthetic (this library's
+counter-based generator: nibbles uniform, d = f16(U(0.005, 0.02))).
+
+Prints one JSON line (rank 0).  The CPU baseline leg times the C oracle's
+restatement of the reference's Q4_0 CPU path (dequantise + f32 GEMV,
+q4_0_cpu_reference_forward) on a bounded sample of the same experts.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import importlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+PKG = "micro-expert-router-ssd-streamed-moe-mer_amd"
+
+HBM_PEAK_GBPS = 8000.0
+Q4_BLOCK = 18
+METRIC = "expert-FFN tokens/s + achieved HBM GB/s (% of peak), Mixtral-shape Q4_0 top-2"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(mer, blob_dev, x_np, dm, dff, experts_per_token, budget_s, gpu_y):
+    """Oracle (checker) timing on host cores: bounded sample of expert FFNs."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import mer_oracle  # noqa: E402  (test infrastructure, used as the checker)
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    times, max_err = [], 0.0
+    n = 0
+    t_start = time.perf_counter()
+    for blob, gy in zip(blob_dev, gpu_y):
+        host = blob.cpu().numpy()
+        t0 = time.perf_counter()
+        y = mer_oracle.q4_0_reference_forward(host, x_np, dm, dff, nthreads=threads)
+        times.append(time.perf_counter() - t0)
+        err = np.abs(y.astype(np.float64) - gy) / (1e-3 + 1e-3 * np.abs(y))
+        max_err = max(max_err, float(err.max()))
+        n += 1
+        if time.perf_counter() - t_start > budget_s:
+            break
+    per_expert = float(np.mean(times))
+    return {
+        "value": 1.0 / (per_expert * experts_per_token),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{n} Mixtral-shape Q4_0 expert FFNs (dequantise + f32 GEMV, the reference's "
+                   f"q4_0_cpu_reference_forward restated in C, {threads} threads), mean "
+                   f"{per_expert * 1e3:.1f} ms/expert, scaled to {experts_per_token} experts/token"),
+        "ms_per_expert": per_expert * 1e3,
+        "parity_worst_ratio": max_err,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=0xC0FFEE)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(experts would shard id % n_gpu; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    mer = importlib.import_module(PKG)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    mer.init(0)
+    lib = mer._lib.lib()
+
+    L, E, K, dm, dff = args.layers, 8, 2, 4096, 14336
+    ebytes = mer.expert_weight_bytes_for(dm, dff, mer.WeightDtype.Q4_0)
+    assert ebytes == 99_090_432
+    nb = ebytes // Q4_BLOCK
+    log(f"allocating {L * E} experts x {ebytes} B = {L * E * ebytes / 1e9:.2f} GB")
+    weights = torch.empty(L * E * ebytes, dtype=torch.uint8, device=dev)
+    for e in range(L * E):
+        mer.fill_synthetic(mer.WeightDtype.Q4_0, args.seed, e, nb, 0.005, 0.02, weights[e * ebytes:(e + 1) * ebytes])
+    torch.cuda.synchronize()
+    base = weights.data_ptr()
+    table = torch.tensor([[base + (l * E + e) * ebytes for e in range(E)] for l in range(L)],
+                         dtype=torch.int64, device=dev)
+
+    routing = importlib.import_module(PKG + ".routing")
+    total_steps = args.warmup + args.steps
+    rng = np.random.default_rng(args.seed + 2)
+    logits = rng.standard_normal((total_steps, L, E)).astype(np.float32)
+    ids = np.zeros((total_steps, L, 1, K), np.int32)
+    wts = np.zeros((total_steps, L, 1, K), np.float32)
+    for s in range(total_steps):
+        for l in range(L):
+            i, w = routing.route_scores(logits[s, l], K)
+            ids[s, l, 0], wts[s, l, 0] = i, w
+    ids_d = torch.from_numpy(ids).to(dev)
+    wts_d = torch.from_numpy(wts).to(dev)
+    xs = np.random.default_rng(args.seed + 1).standard_normal((L, 1, dm)).astype(np.float32)
+    x0 = xs[0]
+    xs_d = torch.from_numpy(xs).to(dev)
+    out = torch.zeros((1, dm), dtype=torch.float32, device=dev)
+
+    stream = torch.cuda.current_stream().cuda_stream
+    fn = lib.mer_hip_moe_forward
+
+    # Pre-bound C-ABI arguments per (step, layer): the timed loop is pure launches.
+    def step_args(s):
+        return [(4, dm, dff, 1, K, table[l].data_ptr(), E, ids_d[s, l].data_ptr(), wts_d[s, l].data_ptr(),
+                 xs_d[l].data_ptr(), out.data_ptr(), 2, stream) for l in range(L)]
+
+    all_args = [step_args(s) for s in range(total_steps)]
+
+    def run_step(s):
+        for a in all_args[s]:
+            rc = fn(*a)
+            if rc:
+                mer.errors.raise_for_status(rc)
+
+    log("warmup")
+    for s in range(args.warmup):
+        run_step(s)
+    torch.cuda.synchronize()
+    mer.take_device_status()
+
+    log(f"timing {args.steps} steps")
+    mer.stage_timing_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.warmup, total_steps):
+        run_step(s)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    stages = mer.stage_timing_read()
+    mer.stage_timing_enable(False)
+    mer.take_device_status()
+    elapsed = t1 - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    tokens_per_s = args.steps / elapsed
+
+    # Algorithmic bytes (packed weights of each distinct expert touched + f32
+    # activations in/out).  Per launch of each stage (K experts per launch):
+    proj = ebytes // 3
+    gate_up_bytes = K * 2 * proj + dm * 4 + K * dff * 4          # weights + x in + h out
+    down_bytes = K * proj + K * dff * 4 + K * 4 * dm * 4          # weights + h in + 4 column-slice partials
+    combine_bytes = K * 4 * dm * 4 + 2 * dm * 4                   # partial slices + out read/write
+    per_layer_bytes = K * ebytes + 3 * dm * 4  # + x_l in, out read + written
+    token_bytes = L * per_layer_bytes
+    stage_bytes = {"gate_up": gate_up_bytes, "down": down_bytes, "combine": combine_bytes}
+    stage_info = {}
+    for name, (ms, cnt) in stages.items():
+        if cnt:
+            avg = ms / cnt
+            stage_info[name] = {"avg_us": avg * 1e3, "launches": cnt,
+                                "gbps": stage_bytes[name] / (avg * 1e-3) / 1e9}
+    dominant = max(stage_info, key=lambda k: stage_info[k]["avg_us"] * stage_info[k]["launches"])
+    dom = stage_info[dominant]
+
+    # Parity of the sampled experts: GPU single-expert forward on x0.
+    sample = [(0, l, int(ids[0, l, 0, i])) for l in range(2) for i in range(K)]
+    blobs = [weights[(l * E + e) * ebytes:(l * E + e + 1) * ebytes] for _, l, e in sample]
+    xdev = torch.from_numpy(x0[0]).to(dev)
+    gpu_y = [mer.q4_0_forward(b, xdev, dm, dff).cpu().numpy().astype(np.float64) for b in blobs]
+
+    result = {
+        "metric": METRIC,
+        "value": tokens_per_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "mixtral-8x7b-moe-decode-q4_0-top2", "layers": L, "experts_per_layer": E,
+                   "top_k": K, "d_model": dm, "d_ff": dff, "batch": 1, "resident_bytes": L * E * ebytes,
+                   "bytes_per_token": token_bytes, "parallelism": "single-gpu"},
+        "hbm_gbps": token_bytes * tokens_per_s / 1e9,
+        "hbm_frac_of_peak": token_bytes * tokens_per_s / 1e9 / HBM_PEAK_GBPS,
+        "roofline": {"bound": "hbm", "kernel": f"proj_kernel ({dominant})", "achieved": dom["gbps"],
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": dom["gbps"] / HBM_PEAK_GBPS,
+                     "traffic": None, "algorithmic_bytes_per_launch": stage_bytes[dominant],
+                     "avg_launch_us": dom["avg_us"]},
+        "stages": stage_info,
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(mer, blobs, x0[0], dm, dff, L * K, args.cpu_seconds, gpu_y)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

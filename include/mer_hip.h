@@ -1,0 +1,187 @@
+/*
+ * mer_hip.h -- C ABI of the MI355X (gfx950) routed-expert SwiGLU FFN.
+ *
+ * Drop-in for the expert-execution slice of MER
+ * (randyap8-wq/Micro-Expert-Router-SSD-Streamed-MoE-MER).  Every entry
+ * point names the reference interface it replaces; paths are relative to
+ * rust-engine/src/ of the reference.
+ *
+ * Conventions
+ *   - Plain pointers and sizes only; no C++ or torch types cross the ABI.
+ *   - Every function returns a mer_status (0 = MER_OK).  A failing call
+ *     records thread-local detail, readable with mer_last_error() /
+ *     mer_last_error_info().  Nothing aborts or throws across the ABI.
+ *   - "d_" pointers are device pointers (hipMalloc'd on the device made
+ *     current by mer_hip_init); "stream" is a hipStream_t passed as
+ *     void* (NULL = the null stream).  Device entry points are
+ *     asynchronous with respect to the host unless stated otherwise.
+ *   - Expert blobs use MER's on-disk layout unchanged: gate || up || down,
+ *     each projection an independently block-rounded stream of GGUF
+ *     blocks (inference.rs:1089-1146); gate/up are [d_ff x d_model] and
+ *     down is [d_model x d_ff], row-major.
+ *   - Re-entrant: calls on different streams may run concurrently; calls
+ *     that share the library's per-device scratch (mer_hip_expert_forward,
+ *     mer_hip_moe_forward) are serialised onto the caller's stream order,
+ *     so concurrent use needs one stream per caller thread and the
+ *     caller must not overlap two such calls on different streams.
+ */
+#ifndef MER_HIP_H
+#define MER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MER_ABI_VERSION 1
+
+/* WeightDtype ordinals (inference.rs:138-236); only the GGUF block
+ * formats on the hot path are accepted by this library. */
+enum mer_dtype {
+  MER_DTYPE_Q4_0 = 4,
+  MER_DTYPE_Q8_0 = 5,
+};
+
+enum mer_status {
+  MER_OK = 0,
+  /* ExpertWeightsError (inference.rs:1153-1188) */
+  MER_ERR_BUFFER_TOO_SMALL = 1,
+  MER_ERR_MISALIGNED = 2,
+  MER_ERR_COMPUTE = 3, /* the Candle(String) slot: a compute-side failure */
+  MER_ERR_INVALID_LAYOUT = 4,
+  MER_ERR_TRUNCATED_PAYLOAD = 5,
+  /* GpuExpertDispatchErrorKind (backend/mod.rs:349-361) */
+  MER_ERR_RESIDENCY_MISS = 16,
+  MER_ERR_PHYSICAL_CAPACITY = 17,
+  MER_ERR_UPLOAD = 18,
+  MER_ERR_VALIDATION_DISPATCH = 19,
+  MER_ERR_SUBMISSION = 20,
+  MER_ERR_READBACK_CHANNEL = 21,
+  MER_ERR_READBACK_MAP = 22,
+  MER_ERR_DEVICE_LOST = 23,
+  MER_ERR_RUNTIME_INVARIANT = 24,
+  /* RoutedExpertGpuIncompatibility (backend/mod.rs:4621-4719) */
+  MER_ERR_UNSUPPORTED_DTYPE = 32,
+  MER_ERR_SHAPE_EXCEEDS_WORKSPACE = 33,
+  /* library state */
+  MER_ERR_NOT_INITIALIZED = 48,
+  MER_ERR_WRONG_DEVICE = 49,
+};
+
+/* Detail of the calling thread's last failure.  For BufferTooSmall and
+ * TruncatedPayload, have/need/d_model/d_ff carry the reference fields
+ * (inference.rs:1157-1186). */
+typedef struct mer_error_info {
+  int32_t status;
+  uint64_t have;
+  uint64_t need;
+  uint64_t d_model;
+  uint64_t d_ff;
+} mer_error_info;
+
+/* Largest d_model / d_ff a routed expert may have on the GPU
+ * (MAX_EXPERT_D_FF, backend/mod.rs:17). */
+#define MER_MAX_EXPERT_DIM 16384
+
+/* ---- library ------------------------------------------------------ */
+int mer_hip_abi_version(void);
+/* Select and initialise a device; fails with MER_ERR_WRONG_DEVICE unless
+ * it is a gfx950 (MI355X).  Replaces GpuBackend construction
+ * (backend/mod.rs:2202-2260). */
+int mer_hip_init(int device);
+int mer_hip_shutdown(void);
+const char *mer_last_error(void);
+int mer_last_error_info(mer_error_info *out);
+/* Device fault word written by kernels (bad expert id, null table entry):
+ * returns the first status recorded since the last reset and clears it.
+ * Synchronises the device. */
+int mer_hip_take_device_status(void);
+
+/* GPU stage timings (the StageTimings analogue, stage_timing.rs:6-29):
+ * while enabled, each expert launch is bracketed by HIP events on its
+ * stream.  read() synchronises the device and returns, per stage
+ * {0 = gate/up + SiLU, 1 = down, 2 = combine}, the summed milliseconds and
+ * launch counts since the last enable/read, then resets.  Timing must not
+ * be enabled while the caller captures a HIP graph. */
+int mer_hip_stage_timing_enable(int enable);
+int mer_hip_stage_timing_read(double *ms /*[3]*/, uint64_t *counts /*[3]*/);
+
+/* ---- host-only sizing and validation (no GPU work) ----------------- */
+/* expert_weight_bytes_for (inference.rs:1089-1146); saturates. */
+size_t mer_expert_weight_bytes(int dtype, size_t d_model, size_t d_ff);
+/* The validation each forward performs before launching:
+ *   Q4_0: from_bytes_q4_0_with_tolerance (inference.rs:1766-1783,
+ *         :4035-4077) then the x-length check forward_candle performs;
+ *   Q8_0: validate_q8_direct_layout (inference.rs:3349-3418). */
+int mer_validate_expert(int dtype, size_t len, size_t x_len, size_t y_len,
+                        size_t d_model, size_t d_ff, size_t tolerance);
+/* routed_expert_gpu_compatibility (backend/mod.rs:4691-4719), extended:
+ * Q8_0 is GPU-eligible here, and any Q4_0 shape is accepted (unaligned
+ * shapes run the generic flat-layout kernel). */
+int mer_routed_expert_gpu_compatibility(int dtype, size_t d_model, size_t d_ff);
+
+/* ---- device entry points ------------------------------------------ */
+/* dequantize_q4_0_to_f32 / dequantize_q8_0_to_f32 (inference.rs:852-868,
+ * :963-979): bit-exact d*(q-8) / d*q, tail block truncated. */
+int mer_hip_dequantize(int dtype, const void *d_src, size_t src_len,
+                       size_t n_weights, float *d_dst, void *stream);
+
+/* Raw Q4_0 qualification matvec (backend/mod.rs:3532-3768,
+ * q4_parity.rs:591-619): rows x columns starting at block w_block_off,
+ * row r at blocks w_block_off + r*columns/32 ..  */
+int mer_hip_q4_0_matvec(const void *d_weights, size_t weights_len,
+                        size_t w_block_off, size_t rows, size_t columns,
+                        const float *d_input, float *d_output, void *stream);
+
+/* One routed expert, VRAM-resident bytes: drop-in for
+ * dispatch_expert_forward's Q4_0 / Q8_0 arms (engine.rs:1761-1848):
+ *   Q4_0 -> q4_0_cpu_reference_forward (inference.rs:3291-3306)
+ *   Q8_0 -> forward_q8_0_direct_into  (inference.rs:3636-3746)
+ * y = W_down (silu(W_gate x) * (W_up x)); fp32 accumulate. */
+int mer_hip_expert_forward(int dtype, const void *d_bytes, size_t len,
+                           const float *d_x, size_t x_len, size_t d_model,
+                           size_t d_ff, float *d_y, size_t y_len, void *stream);
+
+/* Same with host buffers (copies in, runs, copies out, synchronises):
+ * the literal signature of forward_q8_0_direct_into / the Q4_0 reference
+ * over ExpertResident::data() bytes.  PCIe-inclusive. */
+int mer_hip_expert_forward_host(int dtype, const void *bytes, size_t len,
+                                const float *x, size_t x_len, size_t d_model,
+                                size_t d_ff, float *y, size_t y_len);
+
+/* Flags for mer_hip_moe_forward. */
+#define MER_MOE_RESIDUAL 1u   /* out = x + sum_i w_i y_i                */
+#define MER_MOE_ACCUMULATE 2u /* out = out + sum_i w_i y_i              */
+
+/* Fused routed experts + top-k weighted combine for n_tokens decode
+ * tokens: the WeightedInto loop of moe_step_inner (engine.rs:5548-5639)
+ * and routed_expert_matmul_batch_q4 (backend/mod.rs:4401-4418).
+ *   d_expert_table[table_len]  device array of device pointers to expert
+ *                              blobs (NULL = not resident)
+ *   d_expert_ids[n_tokens*top_k], d_weights[n_tokens*top_k]  (device)
+ *   d_x[n_tokens*d_model] in, d_out[n_tokens*d_model] out.
+ * Combine order per token: acc = 0; acc += w_i * y_i for i in slot order
+ * (combine_outputs_into, inference.rs:4472-4491); then the flags.
+ * An id >= table_len or a NULL entry contributes nothing and records
+ * MER_ERR_RESIDENCY_MISS in the device status word. */
+int mer_hip_moe_forward(int dtype, size_t d_model, size_t d_ff,
+                        size_t n_tokens, size_t top_k,
+                        const void *const *d_expert_table, size_t table_len,
+                        const int32_t *d_expert_ids, const float *d_weights,
+                        const float *d_x, float *d_out, unsigned flags,
+                        void *stream);
+
+/* Synthetic bench / test data: fill n_blocks GGUF blocks of expert
+ * `expert_index` starting at block `block_begin` with this library's
+ * counter-based generator (nibbles / int8 uniform, d = f16(U(lo,hi))). */
+int mer_hip_fill_synthetic(int dtype, uint64_t seed, uint64_t expert_index,
+                           uint64_t block_begin, uint64_t n_blocks,
+                           float scale_lo, float scale_hi, void *d_dst,
+                           void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MER_HIP_H */

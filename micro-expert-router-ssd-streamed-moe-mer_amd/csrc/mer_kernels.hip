@@ -1,0 +1,364 @@
+// mer_kernels.hip -- gfx950 kernels of the routed-expert SwiGLU FFN.
+//
+// Hot path (reference inference.rs:3291-3306 / :3636-3746, the expert math
+// behind engine.rs:1761-1848 and the combine of engine.rs:5548-5639):
+//   h_i = silu(W_gate,i x) * (W_up,i x)          proj_kernel<.., FUSED=true>
+//   p_i = W_down,i h_i  (split over column slices) proj_kernel<.., FUSED=false>
+//   out = [x +] sum_i w_i p_i                     combine_kernel
+//
+// Decomposition of proj_kernel.  A wave64 is cut into 64/G lane groups of
+// G lanes (G = 16, 32 or 64).  A lane group owns G*CPL consecutive 64-weight
+// chunks of one column slice and walks down a contiguous row range, R rows
+// per pass; each lane keeps its chunks' input values in registers for the
+// whole walk, so the only per-row traffic is the weight stream itself:
+// every weight byte is read from HBM exactly once, with 16-byte loads.  Row
+// partial sums are reduced across the G lanes with shuffles.  Work items
+// are (expert instance, column slice, row range); their count is sized so
+// the grid holds ~12 waves per CU.
+#include "mer_internal.hpp"
+
+namespace mer {
+
+__device__ uint32_t g_device_status;
+
+__device__ __forceinline__ void record_status(uint32_t code) {
+  atomicCAS(&g_device_status, 0u, code);
+}
+
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Resolve the expert blob of instance `inst`.
+__device__ __forceinline__ const uint8_t *resolve_expert(const ProjParams &p, uint32_t inst) {
+  if (p.single) return p.single;
+  const int32_t id = p.ids[inst];
+  if (id < 0 || (uint32_t)id >= p.table_len) {
+    record_status(16u /* MER_ERR_RESIDENCY_MISS */);
+    return nullptr;
+  }
+  const uint8_t *b = reinterpret_cast<const uint8_t *>(p.table[id]);
+  if (!b) record_status(16u);
+  return b;
+}
+
+template <int FMT, int G, int CPL, int R, bool FUSED>
+__global__ __launch_bounds__(256) void proj_kernel(ProjParams p) {
+  using T = FmtTraits<FMT>;
+  constexpr int kGroups = 64 / G;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t grp = lane / G;
+  const uint32_t gl = lane % G;
+  const uint32_t gwave = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+  const uint32_t per_inst = p.slices * p.waves_per_slice;
+  const uint32_t inst = gwave / per_inst;
+  if (inst >= p.n_inst) return;
+  const uint32_t rem = gwave % per_inst;
+  const uint32_t slice = rem / p.waves_per_slice;
+  const uint32_t wv = rem % p.waves_per_slice;
+  const uint32_t r_begin = wv * p.rows_per_wave;
+  if (r_begin >= p.rows) return;
+  const uint32_t r_end = min(p.rows, r_begin + p.rows_per_wave);
+
+  float *out = p.out + ((size_t)inst * p.slices + slice) * p.rows;
+  const uint8_t *expert = resolve_expert(p, inst);
+  if (!expert) {
+    for (uint32_t r = r_begin + lane; r < r_end; r += 64) out[r] = 0.f;
+    return;
+  }
+  const uint8_t *w0 = expert + p.proj_off0;
+  const uint8_t *w1 = expert + p.proj_off1;  // up projection (FUSED only)
+  const float *x = p.x + (size_t)(inst / p.x_div) * p.x_stride;
+  const size_t row_bytes = (size_t)p.chunks * T::kChunkBytes;
+
+  // chunk ownership and input slice
+  uint32_t chunk[CPL];
+  bool valid[CPL];
+  XSlice<FMT> xs[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const uint32_t local = gl + (uint32_t)i * G;
+    chunk[i] = slice * p.chunks_per_slice + local;
+    valid[i] = local < p.chunks_per_slice && chunk[i] < p.chunks;
+    if (valid[i]) load_xslice<FMT>(x + (size_t)chunk[i] * 64, xs[i]);
+    else zero_xslice<FMT>(xs[i]);
+  }
+
+  constexpr int kStreams = FUSED ? 2 : 1;
+  for (uint32_t r0 = r_begin + grp * R; r0 < r_end; r0 += R * kGroups) {
+    uint32_t wbuf[kStreams][CPL][R][T::kChunkDwords];
+#pragma unroll
+    for (int sidx = 0; sidx < kStreams; ++sidx)
+#pragma unroll
+      for (int i = 0; i < CPL; ++i)
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+          if (valid[i] && r0 + j < r_end) {
+            const uint8_t *base = (sidx == 0 ? w0 : w1) + (size_t)(r0 + j) * row_bytes +
+                                  (size_t)chunk[i] * T::kChunkBytes;
+            load_chunk<FMT>(base, wbuf[sidx][i][j]);
+          } else {
+#pragma unroll
+            for (int k = 0; k < T::kChunkDwords; ++k) wbuf[sidx][i][j][k] = 0x88888888u;
+          }
+        }
+    float acc[kStreams][R];
+#pragma unroll
+    for (int sidx = 0; sidx < kStreams; ++sidx)
+#pragma unroll
+      for (int j = 0; j < R; ++j) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) a += chunk_dot<FMT>(wbuf[sidx][i][j], xs[i]);
+        acc[sidx][j] = group_sum<G>(a);
+      }
+    if (gl == 0) {
+#pragma unroll
+      for (int j = 0; j < R; ++j) {
+        if (r0 + j < r_end) {
+          if constexpr (FUSED) out[r0 + j] = silu_mul(acc[0][j], acc[1][j]);
+          else out[r0 + j] = acc[0][j];
+        }
+      }
+    }
+  }
+}
+
+// Flat-layout fallback for any shape / alignment: one thread per output
+// row, weights decoded element by element in the reference's flat block
+// order (q8_0_matvec_scalar_flat, inference.rs:3618-3632).
+template <int FMT>
+__global__ __launch_bounds__(256) void generic_kernel(ProjParams p, uint32_t cols, int fused) {
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t inst = t / p.rows;
+  if (inst >= p.n_inst) return;
+  const uint32_t r = t % p.rows;
+  float *out = p.out + (size_t)inst * p.rows;
+  const uint8_t *expert = resolve_expert(p, inst);
+  if (!expert) {
+    out[r] = 0.f;
+    return;
+  }
+  const float *x = p.x + (size_t)(inst / p.x_div) * p.x_stride;
+  const uint8_t *g = expert + p.proj_off0;
+  const uint8_t *u = expert + p.proj_off1;
+  float ag = 0.f, au = 0.f;
+  for (uint32_t c = 0; c < cols; ++c) {
+    const size_t flat = (size_t)r * cols + c;
+    const float xv = x[c];
+    ag = __builtin_fmaf(flat_weight<FMT>(g, flat), xv, ag);
+    if (fused) au = __builtin_fmaf(flat_weight<FMT>(u, flat), xv, au);
+  }
+  out[r] = fused ? silu_mul(ag, au) : ag;
+}
+
+// out[t][j] = base + sum_i w[t,i] * sum_s partial[t,i,s][j]
+// base = x (RESIDUAL), out (ACCUMULATE) or 0.  Slots with w == 0 are
+// skipped as in the engine's WeightedInto accumulate (engine.rs:5575-5580).
+__global__ __launch_bounds__(256) void combine_kernel(CombineParams c) {
+  const size_t t_j = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t_j >= (size_t)c.n_tokens * c.d_model) return;
+  const uint32_t t = (uint32_t)(t_j / c.d_model);
+  const uint32_t j = (uint32_t)(t_j % c.d_model);
+  float acc = 0.f;
+  for (uint32_t i = 0; i < c.top_k; ++i) {
+    const float w = c.weights ? c.weights[(size_t)t * c.top_k + i] : 1.0f;
+    if (c.weights && w == 0.0f) continue;
+    const float *pp = c.partial + ((size_t)(t * c.top_k + i) * c.slices) * c.d_model + j;
+    float y = pp[0];
+    for (uint32_t s = 1; s < c.slices; ++s) y += pp[(size_t)s * c.d_model];
+    acc = c.weights ? acc + w * y : acc + y;
+  }
+  float base = 0.f;
+  if (c.flags & 1u) base = c.x[t_j];
+  else if (c.flags & 2u) base = c.out[t_j];
+  c.out[t_j] = (c.flags & 3u) ? base + acc : acc;
+}
+
+// dequantize_*_to_f32: one thread per block; tail block truncated.
+template <int FMT>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *src, size_t n_weights,
+                                                      float *dst) {
+  const size_t blk = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t nblocks = (n_weights + 31) / 32;
+  if (blk >= nblocks) return;
+  const uint8_t *b = src + blk * FmtTraits<FMT>::kBlockBytes;
+  const float d = f16_bits_to_f32((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+  const size_t base = blk * 32;
+  const size_t n = n_weights - base < 32 ? n_weights - base : 32;
+  for (size_t i = 0; i < n; ++i) {
+    float v;
+    if constexpr (FMT == FMT_Q4_0) {
+      const uint8_t byte = b[2 + (i & 15)];
+      v = d * (float)((i < 16 ? (byte & 0x0f) : (byte >> 4)) - 8);
+    } else {
+      v = d * (float)(int8_t)b[2 + i];
+    }
+    dst[base + i] = v;
+  }
+}
+
+// Raw Q4_0 qualification matvec: row r reads blocks w_block_off + r*bpr ..
+__global__ __launch_bounds__(256) void q4_raw_matvec_kernel(const uint8_t *w, size_t w_block_off,
+                                                            uint32_t rows, uint32_t bpr,
+                                                            const float *x, float *y) {
+  const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  float sum = 0.f;
+  for (uint32_t k = 0; k < bpr; ++k) {
+    const uint8_t *b = w + (w_block_off + (size_t)r * bpr + k) * 18;
+    const float d = f16_bits_to_f32((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+    for (int c = 0; c < 32; ++c) {
+      const uint8_t byte = b[2 + (c & 15)];
+      const float wv = d * (float)((c < 16 ? (byte & 0x0f) : (byte >> 4)) - 8);
+      sum = __builtin_fmaf(wv, x[k * 32 + c], sum);
+    }
+  }
+  y[r] = sum;
+}
+
+// Counter-based synthetic generator; byte-for-byte the oracle's
+// mo_bench_fill_q4_0 / mo_bench_fill_q8_0.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+template <int FMT>
+__global__ __launch_bounds__(256) void fill_kernel(uint64_t seed, uint64_t expert, uint64_t block_begin,
+                                                   uint64_t n_blocks, float lo, float hi, uint8_t *dst) {
+  const uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= n_blocks) return;
+  const uint64_t key = seed * 0x9E3779B97F4A7C15ull + expert * 0xD1B54A32D192ED03ull + 9 * (block_begin + k);
+  const float u = (float)(uint32_t)(mix64(key + 8) >> 40) * (1.0f / 16777216.0f);
+  const uint16_t s = f32_to_f16_bits(lo + (hi - lo) * u);
+  uint8_t *o = dst + k * FmtTraits<FMT>::kBlockBytes;
+  uint16_t *o16 = reinterpret_cast<uint16_t *>(o);  // blocks start 2-byte aligned
+  o16[0] = s;
+  if constexpr (FMT == FMT_Q4_0) {
+    const uint64_t a = mix64(key), b = mix64(key + 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o16[1 + i] = (uint16_t)(a >> (16 * i));
+      o16[5 + i] = (uint16_t)(b >> (16 * i));
+    }
+  } else {
+#pragma unroll
+    for (int wi = 0; wi < 8; ++wi) {
+      const uint64_t v = mix64(key + (uint64_t)wi);
+      uint8_t q[4];
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const uint32_t v16 = (uint32_t)(v >> (16 * f)) & 0xffffu;
+        q[f] = (uint8_t)(int8_t)((int)((v16 * 255u) >> 16) - 127);
+      }
+      o16[1 + 2 * wi] = (uint16_t)(q[0] | (q[1] << 8));
+      o16[2 + 2 * wi] = (uint16_t)(q[2] | (q[3] << 8));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------
+// Host-side launchers.
+
+template <int FMT, int G, int CPL, int R, bool FUSED>
+static hipError_t launch_proj_t(const ProjParams &p, hipStream_t st) {
+  const uint32_t waves = p.n_inst * p.slices * p.waves_per_slice;
+  const uint32_t blocks = (waves + 3) / 4;
+  hipLaunchKernelGGL((proj_kernel<FMT, G, CPL, R, FUSED>), dim3(blocks), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+template <int FMT, bool FUSED, int R>
+static hipError_t launch_proj_fmt(const ProjParams &p, int G, int CPL, hipStream_t st) {
+  if (G == 16) return launch_proj_t<FMT, 16, 1, R, FUSED>(p, st);
+  if (G == 32) return launch_proj_t<FMT, 32, 1, R, FUSED>(p, st);
+  // Two register-resident chunks per lane only fit the Q4_0 fused walk
+  // (max_fused_cpl); everything else streams one chunk per lane.
+  if constexpr (FUSED && FMT == FMT_Q4_0) {
+    if (CPL == 2) return launch_proj_t<FMT, 64, 2, R, FUSED>(p, st);
+  }
+  if (CPL != 1) return hipErrorInvalidValue;
+  return launch_proj_t<FMT, 64, 1, R, FUSED>(p, st);
+}
+
+hipError_t launch_proj(int fmt, bool fused, const ProjPlan &plan, const ProjParams &p, hipStream_t st) {
+  if (fmt == FMT_Q4_0) {
+    return fused ? launch_proj_fmt<FMT_Q4_0, true, kFusedRows>(p, plan.G, plan.CPL, st)
+                 : launch_proj_fmt<FMT_Q4_0, false, kDownRows>(p, plan.G, plan.CPL, st);
+  }
+  return fused ? launch_proj_fmt<FMT_Q8_0, true, kFusedRows>(p, plan.G, plan.CPL, st)
+               : launch_proj_fmt<FMT_Q8_0, false, kDownRows>(p, plan.G, plan.CPL, st);
+}
+
+hipError_t launch_generic(int fmt, bool fused, const ProjParams &p, uint32_t cols, hipStream_t st) {
+  const uint64_t threads = (uint64_t)p.n_inst * p.rows;
+  const uint32_t blocks = (uint32_t)((threads + 255) / 256);
+  if (blocks == 0) return hipSuccess;
+  if (fmt == FMT_Q4_0)
+    hipLaunchKernelGGL(generic_kernel<FMT_Q4_0>, dim3(blocks), dim3(256), 0, st, p, cols, fused ? 1 : 0);
+  else
+    hipLaunchKernelGGL(generic_kernel<FMT_Q8_0>, dim3(blocks), dim3(256), 0, st, p, cols, fused ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(const CombineParams &c, hipStream_t st) {
+  const uint64_t n = (uint64_t)c.n_tokens * c.d_model;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(combine_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, c);
+  return hipGetLastError();
+}
+
+hipError_t launch_dequant(int fmt, const uint8_t *src, size_t n_weights, float *dst, hipStream_t st) {
+  const size_t nblocks = (n_weights + 31) / 32;
+  if (nblocks == 0) return hipSuccess;
+  const uint32_t grid = (uint32_t)((nblocks + 255) / 256);
+  if (fmt == FMT_Q4_0) hipLaunchKernelGGL(dequant_kernel<FMT_Q4_0>, dim3(grid), dim3(256), 0, st, src, n_weights, dst);
+  else hipLaunchKernelGGL(dequant_kernel<FMT_Q8_0>, dim3(grid), dim3(256), 0, st, src, n_weights, dst);
+  return hipGetLastError();
+}
+
+hipError_t launch_q4_raw(const uint8_t *w, size_t w_block_off, uint32_t rows, uint32_t bpr,
+                         const float *x, float *y, hipStream_t st) {
+  hipLaunchKernelGGL(q4_raw_matvec_kernel, dim3((rows + 255) / 256), dim3(256), 0, st, w, w_block_off,
+                     rows, bpr, x, y);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill(int fmt, uint64_t seed, uint64_t expert, uint64_t block_begin, uint64_t n_blocks,
+                       float lo, float hi, uint8_t *dst, hipStream_t st) {
+  if (n_blocks == 0) return hipSuccess;
+  const uint64_t grid = (n_blocks + 255) / 256;
+  // keep each launch within a 32-bit grid
+  const uint64_t max_grid = 1ull << 30;
+  for (uint64_t g0 = 0; g0 < grid; g0 += max_grid) {
+    const uint64_t g = grid - g0 < max_grid ? grid - g0 : max_grid;
+    const uint64_t b0 = g0 * 256;
+    const uint64_t nb = n_blocks - b0 < g * 256 ? n_blocks - b0 : g * 256;
+    uint8_t *d = dst + b0 * (fmt == FMT_Q4_0 ? 18 : 34);
+    if (fmt == FMT_Q4_0)
+      hipLaunchKernelGGL(fill_kernel<FMT_Q4_0>, dim3((uint32_t)g), dim3(256), 0, st, seed, expert,
+                         block_begin + b0, nb, lo, hi, d);
+    else
+      hipLaunchKernelGGL(fill_kernel<FMT_Q8_0>, dim3((uint32_t)g), dim3(256), 0, st, seed, expert,
+                         block_begin + b0, nb, lo, hi, d);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t read_and_clear_device_status(uint32_t *out) {
+  uint32_t zero = 0;
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return e;
+  e = hipMemcpyFromSymbol(out, HIP_SYMBOL(g_device_status), sizeof(uint32_t), 0, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return e;
+  return hipMemcpyToSymbol(HIP_SYMBOL(g_device_status), &zero, sizeof(uint32_t), 0, hipMemcpyHostToDevice);
+}
+
+}  // namespace mer

@@ -1,0 +1,212 @@
+"""Routed-expert execution: host-side mirror of MER's expert interface.
+
+Each function names the reference entry point it stands in for (paths
+relative to rust-engine/src/).  Device tensors are torch tensors on the
+current HIP device; all compute runs in libmer_hip.so on the caller's
+current stream.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+
+import torch
+
+from . import _lib
+from .errors import raise_for_status
+
+
+class WeightDtype(enum.IntEnum):
+    """WeightDtype ordinals (inference.rs:138-236) of the GGUF formats."""
+
+    Q4_0 = 4
+    Q8_0 = 5
+
+
+# inference.rs:731-750, kernels/mod.rs:74-75
+Q4_0_BLOCK_ELEMS = 32
+Q4_0_BLOCK_BYTES = 18
+Q4_0_LAYOUT_STANDARD_V1 = "ggml-standard-v1"
+Q8_0_BLOCK_ELEMS = 32
+Q8_0_BLOCK_BYTES = 34
+EXPERT_SIZE_TOLERANCE_BYTES = 4096  # inference.rs:3962
+
+MOE_RESIDUAL = 1
+MOE_ACCUMULATE = 2
+
+
+def _device_index(t: torch.Tensor) -> int:
+    if not t.is_cuda:
+        raise ValueError("expected a device tensor")
+    return t.device.index if t.device.index is not None else torch.cuda.current_device()
+
+
+def _ptr(t: torch.Tensor, dtype: torch.dtype | None = None) -> int:
+    if not t.is_cuda:
+        raise ValueError("expected a device tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"expected {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError("expected a contiguous tensor")
+    return t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _call(name: str, *args, layer: int = 0, expert_id: int = 0) -> None:
+    rc = getattr(_lib.lib(), name)(*args)
+    if rc != 0:
+        raise_for_status(rc, layer, expert_id)
+
+
+def init(device: int | None = None) -> None:
+    """mer_hip_init for `device` (default: torch's current device)."""
+    _lib.ensure_init(torch.cuda.current_device() if device is None else device)
+
+
+def _init_for(t: torch.Tensor) -> None:
+    _lib.ensure_init(_device_index(t))
+
+
+# ---- host-only ---------------------------------------------------------
+
+def expert_weight_bytes_for(d_model: int, d_ff: int, dtype: WeightDtype) -> int:
+    """expert_weight_bytes_for (inference.rs:1089-1146)."""
+    return int(_lib.lib().mer_expert_weight_bytes(int(dtype), d_model, d_ff))
+
+
+def validate_expert(dtype: WeightDtype, length: int, x_len: int, y_len: int, d_model: int, d_ff: int,
+                    tolerance: int = 0) -> None:
+    """Raises the reference's typed error for an invalid expert call."""
+    _call("mer_validate_expert", int(dtype), length, x_len, y_len, d_model, d_ff, tolerance)
+
+
+def routed_expert_gpu_compatibility(dtype: WeightDtype, d_model: int, d_ff: int) -> None:
+    """routed_expert_gpu_compatibility (backend/mod.rs:4691-4719)."""
+    _call("mer_routed_expert_gpu_compatibility", int(dtype), d_model, d_ff)
+
+
+# ---- device ------------------------------------------------------------
+
+def dequantize_to_f32(dtype: WeightDtype, src: torch.Tensor, n_weights: int,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """dequantize_q4_0_to_f32 / dequantize_q8_0_to_f32 (inference.rs:852, :963)."""
+    _init_for(src)
+    if out is None:
+        out = torch.empty(n_weights, dtype=torch.float32, device=src.device)
+    _call("mer_hip_dequantize", int(dtype), _ptr(src, torch.uint8), src.numel(), n_weights,
+          _ptr(out, torch.float32), _stream())
+    return out
+
+
+def q4_0_matvec(weights: torch.Tensor, w_block_off: int, rows: int, columns: int, x: torch.Tensor,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """Raw Q4_0 qualification matvec (backend/mod.rs:3532-3768)."""
+    _init_for(weights)
+    if out is None:
+        out = torch.empty(rows, dtype=torch.float32, device=weights.device)
+    _call("mer_hip_q4_0_matvec", _ptr(weights, torch.uint8), weights.numel(), w_block_off, rows, columns,
+          _ptr(x, torch.float32), _ptr(out, torch.float32), _stream())
+    return out
+
+
+def dispatch_expert_forward(dtype: WeightDtype, resident: torch.Tensor, x: torch.Tensor, d_model: int,
+                            d_ff: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """dispatch_expert_forward's Q4_0 / Q8_0 arms (engine.rs:1761-1848) on
+    VRAM-resident expert bytes: y = W_down (silu(W_gate x) * (W_up x))."""
+    _init_for(resident)
+    if out is None:
+        out = torch.empty(d_model, dtype=torch.float32, device=resident.device)
+    _call("mer_hip_expert_forward", int(dtype), _ptr(resident, torch.uint8), resident.numel(),
+          _ptr(x, torch.float32), x.numel(), d_model, d_ff, _ptr(out, torch.float32), out.numel(), _stream())
+    return out
+
+
+def forward_q8_0_direct_into(resident: torch.Tensor, x: torch.Tensor, d_model: int, d_ff: int,
+                             y: torch.Tensor) -> None:
+    """forward_q8_0_direct_into (inference.rs:3636-3644): caller-owned y."""
+    dispatch_expert_forward(WeightDtype.Q8_0, resident, x, d_model, d_ff, out=y)
+
+
+def q4_0_forward(resident: torch.Tensor, x: torch.Tensor, d_model: int, d_ff: int) -> torch.Tensor:
+    """The device twin of q4_0_cpu_reference_forward (inference.rs:3291-3306)."""
+    return dispatch_expert_forward(WeightDtype.Q4_0, resident, x, d_model, d_ff)
+
+
+def expert_forward_host(dtype: WeightDtype, resident: bytes | bytearray | memoryview, x, d_model: int,
+                        d_ff: int):
+    """Host buffers in, host vector out (synchronous, PCIe-inclusive).
+
+    `resident` is a bytes-like object, `x` a float32 numpy array."""
+    import numpy as np
+
+    init()
+    xa = np.ascontiguousarray(x, dtype=np.float32)
+    buf = (ctypes.c_uint8 * len(resident)).from_buffer_copy(resident) if not isinstance(
+        resident, np.ndarray) else resident.ctypes.data_as(ctypes.c_void_p)
+    y = np.zeros(d_model, dtype=np.float32)
+    _call("mer_hip_expert_forward_host", int(dtype), ctypes.cast(buf, ctypes.c_void_p), len(resident),
+          xa.ctypes.data, xa.size, d_model, d_ff, y.ctypes.data, y.size)
+    return y
+
+
+def moe_forward(dtype: WeightDtype, d_model: int, d_ff: int, table: torch.Tensor, expert_ids: torch.Tensor,
+                weights: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = None, *,
+                residual: bool = False, accumulate: bool = False) -> torch.Tensor:
+    """Routed experts + top-k weighted combine for a decode batch: the
+    WeightedInto loop of moe_step_inner (engine.rs:5548-5639).
+
+    table      int64 [E] device pointers of resident expert blobs (0 = absent)
+    expert_ids int32 [n_tokens, top_k]
+    weights    float32 [n_tokens, top_k]
+    x          float32 [n_tokens, d_model]
+    """
+    _init_for(x)
+    n_tokens, top_k = expert_ids.shape
+    if weights.shape != expert_ids.shape or x.shape != (n_tokens, d_model):
+        raise ValueError("shape mismatch between expert_ids, weights and x")
+    if out is None:
+        out = torch.empty_like(x)
+    flags = (MOE_RESIDUAL if residual else 0) | (MOE_ACCUMULATE if accumulate else 0)
+    _call("mer_hip_moe_forward", int(dtype), d_model, d_ff, n_tokens, top_k, _ptr(table, torch.int64),
+          table.numel(), _ptr(expert_ids, torch.int32), _ptr(weights, torch.float32), _ptr(x, torch.float32),
+          _ptr(out, torch.float32), flags, _stream())
+    return out
+
+
+def fill_synthetic(dtype: WeightDtype, seed: int, expert_index: int, n_blocks: int, scale_lo: float,
+                   scale_hi: float, out: torch.Tensor, block_begin: int = 0) -> torch.Tensor:
+    """This library's counter-based synthetic GGUF block generator."""
+    _init_for(out)
+    bb = Q4_0_BLOCK_BYTES if dtype == WeightDtype.Q4_0 else Q8_0_BLOCK_BYTES
+    if out.numel() < n_blocks * bb:
+        raise ValueError("output buffer too small")
+    _call("mer_hip_fill_synthetic", int(dtype), seed, expert_index, block_begin, n_blocks, scale_lo, scale_hi,
+          _ptr(out, torch.uint8), _stream())
+    return out
+
+
+def take_device_status() -> None:
+    """Raise the first device-side fault recorded since the last call."""
+    init()
+    _call("mer_hip_take_device_status")
+
+
+STAGES = ("gate_up", "down", "combine")
+
+
+def stage_timing_enable(enable: bool = True) -> None:
+    """Start (or stop) GPU stage timing of every expert launch."""
+    init()
+    _call("mer_hip_stage_timing_enable", 1 if enable else 0)
+
+
+def stage_timing_read() -> dict[str, tuple[float, int]]:
+    """{stage: (total_ms, launches)} since the last enable/read (syncs)."""
+    init()
+    ms = (ctypes.c_double * 3)()
+    counts = (ctypes.c_uint64 * 3)()
+    _call("mer_hip_stage_timing_read", ms, counts)
+    return {name: (ms[i], int(counts[i])) for i, name in enumerate(STAGES)}

@@ -1,0 +1,121 @@
+"""The C-ABI library loads, exports every symbol include/mer_hip.h declares,
+and its host-only sizing / validation agrees with the oracle.  CPU only:
+nothing here launches GPU work."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "mer_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mer_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_surface():
+    names = declared_functions()
+    for must in ("mer_hip_init", "mer_hip_expert_forward", "mer_hip_moe_forward", "mer_hip_dequantize",
+                 "mer_hip_q4_0_matvec", "mer_expert_weight_bytes"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(mer):
+    lib = mer._lib.lib()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python binding covers exactly the declared set
+    assert sorted(mer._lib.SIGNATURES) == declared_functions()
+
+
+def test_abi_version(mer):
+    assert mer._lib.lib().mer_hip_abi_version() == 1
+
+
+def test_uninitialised_calls_fail_cleanly(mer):
+    lib = mer._lib.lib()
+    rc = lib.mer_hip_expert_forward(4, None, 0, None, 0, 32, 32, None, 0, None)
+    assert rc == mer._lib.Status.NOT_INITIALIZED
+    assert b"mer_hip_init" in lib.mer_last_error()
+
+
+@pytest.mark.parametrize("dtype,dm,dff", [(4, 8, 8), (4, 10, 10), (5, 8, 8), (4, 4096, 14336), (4, 7168, 2048),
+                                          (5, 2048, 768), (5, 37, 45), (4, 0, 5)])
+def test_expert_weight_bytes_matches_oracle(mer, oracle, dtype, dm, dff):
+    assert mer.expert_weight_bytes_for(dm, dff, mer.WeightDtype(dtype)) == oracle.expert_weight_bytes(dtype, dm, dff)
+
+
+def test_expert_weight_bytes_saturates(mer):
+    assert mer.expert_weight_bytes_for(2**63, 2**63, mer.WeightDtype.Q4_0) == 2**64 - 1
+
+
+def _status(mer, fn):
+    try:
+        fn()
+    except mer.ExpertWeightsError as e:
+        return int(e.status), e
+    return 0, None
+
+
+def test_q8_validation_matches_oracle(mer, oracle):
+    cases = [
+        (0, 0, 0, 0, 2), (10, 31, 32, 32, 32), (0, 2**63, 2**63, 2**63, 2),
+    ]
+    need = oracle.expert_weight_bytes(5, 32, 64)
+    cases += [(need - 1, 32, 32, 32, 64), (need, 32, 32, 32, 64), (need + 7, 32, 32, 32, 64)]
+    small = oracle.expert_weight_bytes(5, 32, 32)
+    cases += [(small - 1, 32, 32, 32, 32)]
+    for length, xl, yl, dm, dff in cases:
+        st, _ = _status(mer, lambda: mer.validate_expert(mer.WeightDtype.Q8_0, length, xl, yl, dm, dff))
+        assert st == oracle.validate_q8_direct(length, xl, yl, dm, dff), (length, xl, yl, dm, dff)
+
+
+def test_q4_validation_matches_oracle_and_reports_fields(mer, oracle):
+    dm, dff = 4096, 14336
+    need = oracle.expert_weight_bytes(4, dm, dff)
+    for length in (need, need + 1, need - 1, need - 4096, need - 4097, 0):
+        st, err = _status(mer, lambda: mer.validate_expert(mer.WeightDtype.Q4_0, length, dm, dm, dm, dff))
+        assert st == oracle.validate_q4_0(length, dm, dff), length
+        if st in (1, 5):
+            assert (err.have, err.need, err.d_model, err.d_ff) == (length, need, dm, dff)
+    # x length mismatch is the Candle shape error of forward_candle
+    st, _ = _status(mer, lambda: mer.validate_expert(mer.WeightDtype.Q4_0, need, dm - 1, dm, dm, dff))
+    assert st == mer._lib.Status.COMPUTE
+    assert isinstance(_status(mer, lambda: mer.validate_expert(mer.WeightDtype.Q4_0, 107, 8, 8, 8, 8))[1],
+                      mer.BufferTooSmall)
+    assert isinstance(
+        _status(mer, lambda: mer.validate_expert(mer.WeightDtype.Q4_0, need - 10, dm, dm, dm, dff))[1],
+        mer.TruncatedPayload)
+
+
+def test_gpu_compatibility_rule(mer):
+    mer.routed_expert_gpu_compatibility(mer.WeightDtype.Q4_0, 4096, 14336)
+    mer.routed_expert_gpu_compatibility(mer.WeightDtype.Q8_0, 2048, 768)
+    mer.routed_expert_gpu_compatibility(mer.WeightDtype.Q4_0, 16384, 16384)
+    with pytest.raises(mer.RoutedExpertGpuIncompatibility):
+        mer.routed_expert_gpu_compatibility(mer.WeightDtype.Q4_0, 16385, 32)
+    with pytest.raises(mer.RoutedExpertGpuIncompatibility):
+        mer._lib.lib().mer_routed_expert_gpu_compatibility(3, 32, 32) and mer.errors.raise_for_status(
+            mer._lib.lib().mer_routed_expert_gpu_compatibility(3, 32, 32))
+
+
+def test_dispatch_error_kind_names(mer):
+    k = mer.GpuExpertDispatchErrorKind
+    assert str(k.ResidencyMiss) == "residency-miss" and str(k.DeviceLost) == "device-lost"
+    assert int(k.ResidencyMiss.value) == 16
+
+
+def test_product_package_does_not_reference_oracle():
+    pkg = os.path.join(ROOT, "micro-expert-router-ssd-streamed-moe-mer_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".hpp", ".cpp", ".h")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "mer_oracle" not in text and "oracle/" not in text, f
