@@ -3,6 +3,7 @@
 // reference's typed errors; device work is enqueued on the caller's stream.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -64,6 +65,7 @@ int fmt_of(int dtype) { return dtype == MER_DTYPE_Q4_0 ? FMT_Q4_0 : FMT_Q8_0; }
 struct DeviceState {
   bool ready = false;
   int cus = 256;
+  uint32_t waves_per_cu = 12;
   float *scratch = nullptr;
   size_t scratch_floats = 0;
 };
@@ -136,30 +138,34 @@ int ensure_scratch(size_t floats, float **out) {
   return MER_OK;
 }
 
-// Choose the decomposition of one projection launch.
-ProjPlan plan_projection(int fmt, size_t rows, size_t cols, uint32_t n_inst, bool fused, bool aligned) {
+// Choose the decomposition of one projection launch.  `waves_per_cu`
+// sets the grid size (default 12, MER_WAVES_PER_CU overrides at init).
+ProjPlan plan_projection(size_t rows, size_t cols, uint32_t n_inst, bool fused, bool aligned) {
   ProjPlan pl{};
-  pl.fast = aligned && cols % 64 == 0 && cols <= MER_MAX_EXPERT_DIM && rows > 0;
-  const uint32_t C = (uint32_t)(cols / 64);
-  if (fused && C > 64u * (uint32_t)max_fused_cpl(fmt)) pl.fast = false;
+  // Fast path: rows of an even number of blocks (4-byte aligned chunks) and
+  // 32-row blocks of h; every configuration of the benchmark qualifies.
+  pl.fast = aligned && cols % 64 == 0 && rows % 64 == 0 && cols <= MER_MAX_EXPERT_DIM &&
+            rows <= MER_MAX_EXPERT_DIM && rows > 0;
   if (!pl.fast) return pl;
+  const uint32_t C = (uint32_t)(cols / 64);
   if (C <= 16) { pl.G = 16; pl.CPL = 1; pl.slices = 1; }
   else if (C <= 32) { pl.G = 32; pl.CPL = 1; pl.slices = 1; }
   else if (fused) { pl.G = 64; pl.CPL = (int)div_ceil(C, 64); pl.slices = 1; }
   else { pl.G = 64; pl.CPL = 1; pl.slices = (uint32_t)div_ceil(C, 64); }
   pl.chunks_per_slice = (uint32_t)div_ceil(C, pl.slices);
-  const int R = fused ? kFusedRows : kDownRows;
-  const uint32_t unit = (uint32_t)R * (64u / (uint32_t)pl.G);
-  const uint32_t cus = (uint32_t)g_dev[g_device].cus;
-  const uint64_t target_waves = (uint64_t)cus * 12u;
+  const uint32_t R = fused ? kFusedRows : kDownRows;
+  // rows of a wave: whole passes of all lane groups, and (gate/up) whole
+  // 32-row blocks of h per 4-wave workgroup
+  uint32_t unit = R * (64u / (uint32_t)pl.G);
+  while (unit % 8) unit *= 2;
+  const uint64_t target_waves = (uint64_t)g_dev[g_device].cus * g_dev[g_device].waves_per_cu;
   const uint64_t per_slice = (uint64_t)n_inst * pl.slices;
   uint64_t want = target_waves / per_slice;
-  if (want < 1) want = 1;
+  if (want < 4) want = 4;
   uint64_t rpw = div_ceil(rows, want);
   rpw = div_ceil(rpw, unit) * unit;
-  if (rpw < unit) rpw = unit;
   pl.rows_per_wave = (uint32_t)rpw;
-  pl.waves_per_slice = (uint32_t)div_ceil(rows, rpw);
+  pl.wgs_per_slice = (uint32_t)div_ceil(rows, 4 * rpw);
   return pl;
 }
 
@@ -210,18 +216,26 @@ int run_experts(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
   const size_t proj = div_ceil(dm * dff, 32) * block_bytes(dtype);
   const bool aligned = single ? ((uintptr_t)single % 4 == 0) : true;
 
-  ProjPlan pg = plan_projection(fmt, dff, dm, n_inst, true, aligned);
-  ProjPlan pd = plan_projection(fmt, dm, dff, n_inst, false, aligned);
-  const uint32_t slices = pd.fast ? pd.slices : 1;
+  ProjPlan pg = plan_projection(dff, dm, n_inst, true, aligned);
+  ProjPlan pd = plan_projection(dm, dff, n_inst, false, aligned);
+  const bool fast = pg.fast && pd.fast;
+  const uint32_t slices = fast ? pd.slices : 1;
 
   const bool write_direct = direct_out && slices == 1 && n_inst == 1 && flags == 0;
-  const size_t h_floats = (size_t)n_inst * dff;
+  // scratch: f32 h (generic path) | h digit planes + scales (fast path) | partials
+  const size_t hblocks = dff / 32;
+  const size_t h_floats = fast ? 0 : (size_t)n_inst * dff;
+  const size_t hq_dwords = fast ? (size_t)n_inst * hblocks * kBlockDigitDwords : 0;
+  const size_t hs_floats = fast ? (size_t)n_inst * hblocks : 0;
   const size_t p_floats = write_direct ? 0 : (size_t)n_inst * slices * dm;
+  auto up64 = [](size_t v) { return (v + 63) / 64 * 64; };
   float *scratch = nullptr;
-  int rc = ensure_scratch(h_floats + p_floats + 64, &scratch);
+  int rc = ensure_scratch(up64(h_floats) + up64(hq_dwords) + up64(hs_floats) + up64(p_floats), &scratch);
   if (rc) return rc;
   float *h = scratch;
-  float *partial = write_direct ? out : scratch + ((h_floats + 63) / 64) * 64;
+  uint32_t *hq_dig = reinterpret_cast<uint32_t *>(scratch + up64(h_floats));
+  float *hq_scale = scratch + up64(h_floats) + up64(hq_dwords);
+  float *partial = write_direct ? out : hq_scale + up64(hs_floats);
 
   ProjParams p{};
   p.table = table;
@@ -230,7 +244,7 @@ int run_experts(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
   p.single = single;
   p.n_inst = n_inst;
 
-  // gate/up + SiLU -> h
+  // gate/up + SiLU -> h (digit planes on the fast path)
   p.proj_off0 = 0;
   p.proj_off1 = proj;
   p.rows = (uint32_t)dff;
@@ -238,18 +252,23 @@ int run_experts(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
   p.x = x;
   p.x_div = top_k;
   p.x_stride = dm;
-  p.out = h;
+  p.hq_dig = hq_dig;
+  p.hq_scale = hq_scale;
+  p.hq_blocks = (uint32_t)hblocks;
   hipError_t e;
   TimedLaunch *tl = nullptr;
   int trc = timing_begin(STAGE_GATE_UP, st, &tl);
   if (trc) return trc;
-  if (pg.fast) {
+  if (fast) {
+    p.out = nullptr;
     p.slices = 1;
     p.chunks_per_slice = pg.chunks_per_slice;
-    p.waves_per_slice = pg.waves_per_slice;
+    p.wgs_per_slice = pg.wgs_per_slice;
     p.rows_per_wave = pg.rows_per_wave;
+    p.lds_blocks = 2 * pg.chunks_per_slice;
     e = launch_proj(fmt, true, pg, p, st);
   } else {
+    p.out = h;
     p.slices = 1;
     e = launch_generic(fmt, true, p, (uint32_t)dm, st);
   }
@@ -264,13 +283,17 @@ int run_experts(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
   p.x = h;
   p.x_div = 1;
   p.x_stride = dff;
+  p.xq_dig = hq_dig;
+  p.xq_scale = hq_scale;
+  p.xq_blocks = (uint32_t)hblocks;
   p.out = partial;
   if ((trc = timing_begin(STAGE_DOWN, st, &tl))) return trc;
-  if (pd.fast) {
+  if (fast) {
     p.slices = pd.slices;
     p.chunks_per_slice = pd.chunks_per_slice;
-    p.waves_per_slice = pd.waves_per_slice;
+    p.wgs_per_slice = pd.wgs_per_slice;
     p.rows_per_wave = pd.rows_per_wave;
+    p.lds_blocks = 2 * pd.chunks_per_slice;
     e = launch_proj(fmt, false, pd, p, st);
   } else {
     p.slices = 1;
@@ -317,6 +340,10 @@ int mer_hip_init(int device) {
   e = hipSetDevice(device);
   if (e != hipSuccess) return hip_fail(e, MER_ERR_DEVICE_LOST, "hipSetDevice");
   g_dev[device].cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+  if (const char *w = getenv("MER_WAVES_PER_CU")) {
+    const long v = strtol(w, nullptr, 10);
+    if (v >= 1 && v <= 64) g_dev[device].waves_per_cu = (uint32_t)v;
+  }
   g_dev[device].ready = true;
   g_device = device;
   return ok();

@@ -16,13 +16,8 @@
 //   Q8_0 chunk dwords w0..w16: block0 d = w0[15:0], q = bytes 2..33
 //     (realigned from w0..w8); block1 d = w8[31:16], q = w9..w16.
 //
-// Dot products avoid a per-weight subtract: a block contributes
-//   Q4_0: d * (sum_j q_j x_j - 8 * sum_j x_j)          q_j in 0..15
-//   Q8_0: d * (sum_j u_j x_j - 128 * sum_j x_j)        u_j = q_j + 128
-// where each integer converts to f32 with one v_cvt_f32_ubyteN.  High
-// Q4 nibbles are used in place (byte & 0xF0 == 16 q) against x/16, which
-// is exact in binary floating point.  The per-block input sums are
-// computed once per lane and reused for every row the lane visits.
+// Dot products run on packed integer dot instructions against the input
+// vector in block fixed point (see "xq" below).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -100,88 +95,165 @@ __device__ __forceinline__ void load_chunk(const uint8_t *p, uint32_t (&w)[FmtTr
   w[4 * kVec] = reinterpret_cast<const uint32_t *>(p)[4 * kVec];
 }
 
-// Per-lane copy of the input slice for one chunk, pre-transformed.
-//   Q4_0: xv[b*32 + j]      = x[j]        (j < 16, low nibbles)
-//         xv[b*32 + 16 + j] = x[16+j]/16  (high nibbles used as 16 q)
-//         bias[b] = 8 * sum(x over block b)
-//   Q8_0: xv = x, bias[b] = 128 * sum(x over block b)
-template <int FMT> struct XSlice {
-  float xv[64];
-  float bias[2];
+// ---------------------------------------------------------------------
+// Input vectors in block fixed point ("xq").
+//
+// Each 32-element block b of an input vector (x for gate/up, h for down) is
+// stored as x ~= s_b * x_int with s_b = max|x_b| / (2^22 - 1) and
+// |x_int| <= 2^22 - 1 (rounded to nearest): the representation error is at
+// most 2^-23 of the block maximum, the size of an f32 rounding of that
+// element.  x_int is split into signed digits laid out so that one packed
+// integer dot instruction consumes one weight dword:
+//   Q4_0: six balanced base-16 digits (-8..7, 4-bit two's complement).
+//         Digit plane k, group m (0..3) is a dword whose nibble 2t is the
+//         digit of element 4m+t and nibble 2t+1 that of element 4m+16+t --
+//         exactly the element order of qs dword m (byte t = qs[4m+t]).
+//         dot8(qs_m ^ 0x88888888, plane[k][m]) then sums (q-8)*digit over
+//         eight weights (q ^ 8 is q-8 as a 4-bit two's complement value).
+//   Q8_0: three balanced base-256 digits (-128..127).  Plane k, group m
+//         (0..7): byte t is the digit of element 4m+t; dot4 with the raw
+//         int8 weight dword m.
+// Per block: 24 digit dwords, index [k * groups + m], plus s_b.
+// Balanced digits come for free from offset binary: with
+// u = x_int + 0x888888 (resp. 0x808080), digit k = nibble_k(u) ^ 8
+// (resp. byte_k(u) ^ 0x80), i.e. the digit-k field of u ^ 0x888888
+// (resp. u ^ 0x808080).  Integer accumulation is exact; the three (Q8) or
+// six (Q4) per-block digit sums are recombined in f32 once per block.
+constexpr int kBlockDigitDwords = 24;
+constexpr float kXIntMax = 4194303.0f;  // 2^22 - 1
+
+template <int FMT> struct DigitTraits;
+template <> struct DigitTraits<FMT_Q4_0> {
+  static constexpr int kGroups = 4;     // groups of 8 elements per block
+  static constexpr int kGroupElems = 8;
+  static constexpr int kPlanes = 6;
+};
+template <> struct DigitTraits<FMT_Q8_0> {
+  static constexpr int kGroups = 8;     // groups of 4 elements per block
+  static constexpr int kGroupElems = 4;
+  static constexpr int kPlanes = 3;
 };
 
-template <int FMT>
-__device__ __forceinline__ void load_xslice(const float *x, XSlice<FMT> &s) {
-  const float4 *x4 = reinterpret_cast<const float4 *>(x);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    float4 v = x4[i];
-    s.xv[4 * i + 0] = v.x;
-    s.xv[4 * i + 1] = v.y;
-    s.xv[4 * i + 2] = v.z;
-    s.xv[4 * i + 3] = v.w;
-  }
-#pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    float sum = 0.f;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) sum += s.xv[b * 32 + j];
-    s.bias[b] = (FMT == FMT_Q4_0 ? 8.f : 128.f) * sum;
-    if (FMT == FMT_Q4_0) {
-#pragma unroll
-      for (int j = 16; j < 32; ++j) s.xv[b * 32 + j] *= 0.0625f;
-    }
-  }
-}
+struct BlockScale {
+  float s;    // dequantisation scale of the block (NaN if non-finite input)
+  float inv;  // quantisation multiplier
+};
 
-template <int FMT>
-__device__ __forceinline__ void zero_xslice(XSlice<FMT> &s) {
-#pragma unroll
-  for (int i = 0; i < 64; ++i) s.xv[i] = 0.f;
-  s.bias[0] = s.bias[1] = 0.f;
-}
-
-__device__ __forceinline__ float fma_bytes(uint32_t u, const float *x, float a) {
-  a = __builtin_fmaf((float)(u & 0xffu), x[0], a);
-  a = __builtin_fmaf((float)((u >> 8) & 0xffu), x[1], a);
-  a = __builtin_fmaf((float)((u >> 16) & 0xffu), x[2], a);
-  a = __builtin_fmaf((float)(u >> 24), x[3], a);
-  return a;
-}
-
-// sum_j q_j x_j over one Q4_0 block given its four qs dwords.
-__device__ __forceinline__ float q4_block_raw(const uint32_t (&q)[4], const float *xv) {
-  float a = 0.f;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    a = fma_bytes(q[k] & 0x0f0f0f0fu, xv + 4 * k, a);
-    a = fma_bytes(q[k] & 0xf0f0f0f0u, xv + 16 + 4 * k, a);
-  }
-  return a;
-}
-
-template <int FMT>
-__device__ __forceinline__ float chunk_dot(const uint32_t (&w)[FmtTraits<FMT>::kChunkDwords],
-                                           const XSlice<FMT> &s) {
-  if constexpr (FMT == FMT_Q4_0) {
-    const float d0 = f16_bits_to_f32(w[0] & 0xffffu);
-    const float d1 = f16_bits_to_f32(w[4] >> 16);
-    uint32_t q0[4] = {realign16(w[0], w[1]), realign16(w[1], w[2]), realign16(w[2], w[3]),
-                      realign16(w[3], w[4])};
-    uint32_t q1[4] = {w[5], w[6], w[7], w[8]};
-    float a0 = q4_block_raw(q0, s.xv);
-    float a1 = q4_block_raw(q1, s.xv + 32);
-    return __builtin_fmaf(d1, a1 - s.bias[1], d0 * (a0 - s.bias[0]));
+__device__ __forceinline__ BlockScale make_block_scale(float amax, bool finite) {
+  BlockScale b;
+  if (!finite) {
+    b.s = __builtin_nanf("");
+    b.inv = 0.f;
+  } else if (amax == 0.f) {
+    b.s = 0.f;
+    b.inv = 0.f;
   } else {
-    const float d0 = f16_bits_to_f32(w[0] & 0xffffu);
-    const float d1 = f16_bits_to_f32(w[8] >> 16);
-    float a0 = 0.f, a1 = 0.f;
+    b.s = amax / kXIntMax;
+    b.inv = kXIntMax / amax;
+  }
+  return b;
+}
+
+__device__ __forceinline__ int32_t quantize_elem(float v, float inv) {
+  float q = __builtin_rintf(v * inv);
+  q = __builtin_fminf(__builtin_fmaxf(q, -kXIntMax), kXIntMax);
+  return (int32_t)q;
+}
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t v, int k) { return (v >> (8 * k)) & 0xffu; }
+
+// Element index (within its block) of slot i of group m.
+template <int FMT>
+__device__ __forceinline__ int group_elem(int m, int i) {
+  if constexpr (FMT == FMT_Q4_0) return (i & 1) ? 4 * m + 16 + (i >> 1) : 4 * m + (i >> 1);
+  else return 4 * m + i;
+}
+
+// Pack one group (8 elements for Q4_0, 4 for Q8_0, in group slot order)
+// into its digit-plane dwords: plane[k] goes to digit dword k*groups + m.
+template <int FMT>
+__device__ __forceinline__ void pack_group(const float *v, float inv, uint32_t *plane) {
+  if constexpr (FMT == FMT_Q4_0) {
+    uint32_t t[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      a0 = fma_bytes(realign16(w[k], w[k + 1]) ^ 0x80808080u, s.xv + 4 * k, a0);
-      a1 = fma_bytes(w[9 + k] ^ 0x80808080u, s.xv + 32 + 4 * k, a1);
+    for (int i = 0; i < 8; ++i) t[i] = ((uint32_t)(quantize_elem(v[i], inv) + 0x888888)) ^ 0x888888u;
+    uint32_t E[4], O[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t a = t[2 * j], b = t[2 * j + 1];
+      E[j] = (a & 0x0f0f0fu) | ((b << 4) & 0xf0f0f0u);
+      O[j] = ((a >> 4) & 0x0f0f0fu) | (b & 0xf0f0f0u);
     }
-    return __builtin_fmaf(d1, a1 - s.bias[1], d0 * (a0 - s.bias[0]));
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      plane[2 * k] = byte_of(E[0], k) | (byte_of(E[1], k) << 8) | (byte_of(E[2], k) << 16) | (byte_of(E[3], k) << 24);
+      plane[2 * k + 1] = byte_of(O[0], k) | (byte_of(O[1], k) << 8) | (byte_of(O[2], k) << 16) | (byte_of(O[3], k) << 24);
+    }
+  } else {
+    uint32_t t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] = ((uint32_t)(quantize_elem(v[i], inv) + 0x808080)) ^ 0x808080u;
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      plane[k] = byte_of(t[0], k) | (byte_of(t[1], k) << 8) | (byte_of(t[2], k) << 16) | (byte_of(t[3], k) << 24);
+  }
+}
+
+// One block's integer dot, recombined to f32: sum_j w_int_j * x_int_j
+// with w_int = q-8 (Q4_0) or q (Q8_0).  `q` holds the block's weight dwords
+// (4 qs dwords for Q4_0, 8 int8 dwords for Q8_0), `dig` its 24 digit dwords.
+template <int FMT>
+__device__ __forceinline__ float block_idot(const uint32_t *q, const uint32_t *dig) {
+  if constexpr (FMT == FMT_Q4_0) {
+    int a[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      a[k] = 0;
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        a[k] = __builtin_amdgcn_sdot8((int)(q[m] ^ 0x88888888u), (int)dig[k * 4 + m], a[k], false);
+    }
+    // |a_k| <= 2048: pairwise base-16 sums fit easily; p0 + 256*p1 < 2^24
+    const int p0 = a[0] + (a[1] << 4);
+    const int p1 = a[2] + (a[3] << 4);
+    const int p2 = a[4] + (a[5] << 4);
+    const int lo = p0 + (p1 << 8);
+    return __builtin_fmaf((float)p2, 65536.0f, (float)lo);
+  } else {
+    int a[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      a[k] = 0;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) a[k] = __builtin_amdgcn_sdot4((int)q[m], (int)dig[k * 8 + m], a[k], false);
+    }
+    return __builtin_fmaf((float)a[2], 65536.0f, __builtin_fmaf((float)a[1], 256.0f, (float)a[0]));
+  }
+}
+
+// Dot of one 64-weight chunk (two blocks) with its input digits.
+// dig: 48 dwords (block 0 then block 1), sc: the two block scales.
+template <int FMT>
+__device__ __forceinline__ float chunk_idot(const uint32_t (&w)[FmtTraits<FMT>::kChunkDwords], const uint32_t *dig,
+                                            const float *sc) {
+  if constexpr (FMT == FMT_Q4_0) {
+    const uint32_t q0[4] = {realign16(w[0], w[1]), realign16(w[1], w[2]), realign16(w[2], w[3]),
+                            realign16(w[3], w[4])};
+    const uint32_t q1[4] = {w[5], w[6], w[7], w[8]};
+    const float v0 = block_idot<FMT>(q0, dig);
+    const float v1 = block_idot<FMT>(q1, dig + kBlockDigitDwords);
+    const float d0 = f16_bits_to_f32(w[0] & 0xffffu) * sc[0];
+    const float d1 = f16_bits_to_f32(w[4] >> 16) * sc[1];
+    return __builtin_fmaf(d1, v1, d0 * v0);
+  } else {
+    uint32_t q0[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) q0[k] = realign16(w[k], w[k + 1]);
+    const float v0 = block_idot<FMT>(q0, dig);
+    const float v1 = block_idot<FMT>(&w[9], dig + kBlockDigitDwords);
+    const float d0 = f16_bits_to_f32(w[0] & 0xffffu) * sc[0];
+    const float d1 = f16_bits_to_f32(w[8] >> 16) * sc[1];
+    return __builtin_fmaf(d1, v1, d0 * v0);
   }
 }
 

@@ -14,8 +14,9 @@ namespace mer {
 // streams 4 rows.
 constexpr int kFusedRows = 2;
 constexpr int kDownRows = 4;
-// Chunks a lane may keep register-resident in the fused gate/up walk.
-constexpr int max_fused_cpl(int fmt) { return fmt == FMT_Q4_0 ? 2 : 1; }
+// Chunks a lane walks per row (G = 64); inputs beyond one chunk are read
+// from LDS per pass.
+constexpr int kMaxCpl = 4;
 
 // Arguments of one projection launch (passed by value).
 struct ProjParams {
@@ -30,18 +31,29 @@ struct ProjParams {
   uint32_t chunks;           // 64-weight chunks per row
   uint32_t slices;           // column slices
   uint32_t chunks_per_slice;
-  uint32_t waves_per_slice;  // waves walking one (instance, slice)
-  uint32_t rows_per_wave;
-  const float *x;            // input vectors
+  uint32_t wgs_per_slice;    // workgroups walking one (instance, slice)
+  uint32_t rows_per_wave;    // rows of one wave (a workgroup owns 4x)
+  uint32_t lds_blocks;       // input blocks staged in LDS per workgroup
+  const float *x;            // f32 input vectors (gate/up; generic kernel)
   uint32_t x_div;            // input index = instance / x_div
   size_t x_stride;           // floats between consecutive inputs
-  float *out;                // [n_inst][slices][rows]
+  const uint32_t *xq_dig;    // packed inputs of the down projection
+  const float *xq_scale;     //   [n_inst][xq_blocks] digit planes / scales
+  uint32_t xq_blocks;
+  uint32_t *hq_dig;          // packed h written by the gate/up kernel
+  float *hq_scale;           //   [n_inst][hq_blocks]
+  uint32_t hq_blocks;
+  float *out;                // down: [n_inst][slices][rows]; gate/up: f32 h or null
 };
+
+inline size_t proj_lds_bytes(const ProjParams &p, bool fused) {
+  return (size_t)p.lds_blocks * (kBlockDigitDwords * 4 + 4) + (fused ? (size_t)4 * p.rows_per_wave * 4 : 0);
+}
 
 struct ProjPlan {
   bool fast;
   int G, CPL;
-  uint32_t slices, chunks_per_slice, waves_per_slice, rows_per_wave;
+  uint32_t slices, chunks_per_slice, wgs_per_slice, rows_per_wave;
 };
 
 struct CombineParams {

@@ -6,15 +6,17 @@
 //   p_i = W_down,i h_i  (split over column slices) proj_kernel<.., FUSED=false>
 //   out = [x +] sum_i w_i p_i                     combine_kernel
 //
-// Decomposition of proj_kernel.  A wave64 is cut into 64/G lane groups of
-// G lanes (G = 16, 32 or 64).  A lane group owns G*CPL consecutive 64-weight
-// chunks of one column slice and walks down a contiguous row range, R rows
-// per pass; each lane keeps its chunks' input values in registers for the
-// whole walk, so the only per-row traffic is the weight stream itself:
-// every weight byte is read from HBM exactly once, with 16-byte loads.  Row
-// partial sums are reduced across the G lanes with shuffles.  Work items
-// are (expert instance, column slice, row range); their count is sized so
-// the grid holds ~12 waves per CU.
+// Decomposition of proj_kernel.  A workgroup (4 waves) owns one (expert
+// instance, column slice, row range).  It first brings its slice of the
+// input vector into LDS as block fixed-point digit planes (quantising x
+// itself in the gate/up kernel; copying the h planes the gate/up kernel
+// produced in the down kernel).  A wave64 is cut into 64/G lane groups of G
+// lanes (G = 16, 32 or 64); a lane group owns G*CPL consecutive 64-weight
+// chunks of the slice and walks down the wave's rows, R rows per pass,
+// streaming each weight byte from HBM exactly once with 16-byte loads and
+// consuming it with packed integer dot instructions.  Row sums are reduced
+// across the G lanes with shuffles.  The gate/up kernel finally packs its
+// rows of h = silu(g) * u into digit planes for the down kernel.
 #include "mer_internal.hpp"
 
 namespace mer {
@@ -45,49 +47,145 @@ __device__ __forceinline__ const uint8_t *resolve_expert(const ProjParams &p, ui
   return b;
 }
 
+// Quantise `nblocks` 32-element blocks of the f32 vector `x` into digit
+// planes (dig, 24 dwords per block) and block scales (scale).  All threads
+// of the workgroup call this with the same arguments; the kGroups threads
+// of one block are adjacent lanes of one wave and share its max by shuffles.
+template <int FMT>
+__device__ __forceinline__ void pack_vector(const float *x, uint32_t nblocks, uint32_t *dig, float *scale) {
+  using D = DigitTraits<FMT>;
+  const uint32_t ngroups = nblocks * D::kGroups;
+  for (uint32_t base = 0; base < ngroups; base += blockDim.x) {
+    const uint32_t g = base + threadIdx.x;
+    const bool valid = g < ngroups;
+    const uint32_t b = g / D::kGroups, m = g % D::kGroups;
+    float v[D::kGroupElems];
+    float amax = 0.f;
+    int finite = 1;
+    if (valid) {
+      const float *xb = x + (size_t)b * 32;
+      if constexpr (FMT == FMT_Q4_0) {
+        const float4 lo = *reinterpret_cast<const float4 *>(xb + 4 * m);
+        const float4 hi = *reinterpret_cast<const float4 *>(xb + 16 + 4 * m);
+        v[0] = lo.x; v[1] = hi.x; v[2] = lo.y; v[3] = hi.y;
+        v[4] = lo.z; v[5] = hi.z; v[6] = lo.w; v[7] = hi.w;
+      } else {
+        const float4 a = *reinterpret_cast<const float4 *>(xb + 4 * m);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      }
+#pragma unroll
+      for (int i = 0; i < D::kGroupElems; ++i) {
+        amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
+        finite &= __builtin_isfinite(v[i]) ? 1 : 0;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < D::kGroupElems; ++i) v[i] = 0.f;
+    }
+#pragma unroll
+    for (int off = 1; off < D::kGroups; off <<= 1) {
+      amax = __builtin_fmaxf(amax, __shfl_xor(amax, off, 64));
+      finite &= __shfl_xor(finite, off, 64);
+    }
+    if (valid) {
+      const BlockScale bs = make_block_scale(amax, finite != 0);
+      uint32_t plane[D::kPlanes];
+      pack_group<FMT>(v, bs.inv, plane);
+#pragma unroll
+      for (int k = 0; k < D::kPlanes; ++k) dig[(size_t)b * kBlockDigitDwords + k * D::kGroups + m] = plane[k];
+      if (m == 0) scale[b] = bs.s;
+    }
+  }
+}
+
 template <int FMT, int G, int CPL, int R, bool FUSED>
 __global__ __launch_bounds__(256) void proj_kernel(ProjParams p) {
   using T = FmtTraits<FMT>;
   constexpr int kGroups = 64 / G;
+  constexpr int kStreams = FUSED ? 2 : 1;
+  extern __shared__ uint32_t smem[];
+  uint32_t *s_dig = smem;
+  float *s_scale = reinterpret_cast<float *>(smem + (size_t)p.lds_blocks * kBlockDigitDwords);
+  float *s_h = s_scale + p.lds_blocks;
+
+  const uint32_t per_inst = p.slices * p.wgs_per_slice;
+  const uint32_t inst = blockIdx.x / per_inst;
+  const uint32_t rem = blockIdx.x % per_inst;
+  const uint32_t slice = rem / p.wgs_per_slice;
+  const uint32_t wgi = rem % p.wgs_per_slice;
+  const uint32_t wave = threadIdx.x / 64u;
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t grp = lane / G;
   const uint32_t gl = lane % G;
-  const uint32_t gwave = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
-  const uint32_t per_inst = p.slices * p.waves_per_slice;
-  const uint32_t inst = gwave / per_inst;
-  if (inst >= p.n_inst) return;
-  const uint32_t rem = gwave % per_inst;
-  const uint32_t slice = rem / p.waves_per_slice;
-  const uint32_t wv = rem % p.waves_per_slice;
-  const uint32_t r_begin = wv * p.rows_per_wave;
-  if (r_begin >= p.rows) return;
+  const uint32_t rows_per_wg = 4u * p.rows_per_wave;
+  const uint32_t wg_r0 = wgi * rows_per_wg;
+  const uint32_t wg_rows = min(rows_per_wg, p.rows - wg_r0);
+  const uint32_t r_begin = wg_r0 + wave * p.rows_per_wave;
   const uint32_t r_end = min(p.rows, r_begin + p.rows_per_wave);
+  const uint32_t c_begin = slice * p.chunks_per_slice;
+  const uint32_t c_count = min(p.chunks_per_slice, p.chunks - c_begin);
 
-  float *out = p.out + ((size_t)inst * p.slices + slice) * p.rows;
   const uint8_t *expert = resolve_expert(p, inst);
-  if (!expert) {
-    for (uint32_t r = r_begin + lane; r < r_end; r += 64) out[r] = 0.f;
+  if (!expert) {  // uniform over the workgroup: zero this workgroup's outputs
+    if constexpr (FUSED) {
+      const size_t b0 = (size_t)inst * p.hq_blocks + wg_r0 / 32;
+      for (uint32_t i = threadIdx.x; i < wg_rows / 32 * kBlockDigitDwords; i += blockDim.x)
+        p.hq_dig[b0 * kBlockDigitDwords + i] = 0u;
+      for (uint32_t i = threadIdx.x; i < wg_rows / 32; i += blockDim.x) p.hq_scale[b0 + i] = 0.f;
+    } else {
+      float *out = p.out + ((size_t)inst * p.slices + slice) * p.rows;
+      for (uint32_t r = wg_r0 + threadIdx.x; r < wg_r0 + wg_rows; r += blockDim.x) out[r] = 0.f;
+    }
     return;
   }
+
+  // 1. this slice of the input vector -> LDS digit planes
+  if constexpr (FUSED) {
+    const float *x = p.x + (size_t)(inst / p.x_div) * p.x_stride + (size_t)c_begin * 64;
+    pack_vector<FMT>(x, 2 * c_count, s_dig, s_scale);
+  } else {
+    const size_t b0 = (size_t)inst * p.xq_blocks + 2 * (size_t)c_begin;
+    const uint4 *src = reinterpret_cast<const uint4 *>(p.xq_dig + b0 * kBlockDigitDwords);
+    uint4 *dst = reinterpret_cast<uint4 *>(s_dig);
+    const uint32_t n16 = 2 * c_count * kBlockDigitDwords / 4;
+    for (uint32_t i = threadIdx.x; i < n16; i += blockDim.x) dst[i] = src[i];
+    for (uint32_t i = threadIdx.x; i < 2 * c_count; i += blockDim.x) s_scale[i] = p.xq_scale[b0 + i];
+  }
+  __syncthreads();
+
   const uint8_t *w0 = expert + p.proj_off0;
   const uint8_t *w1 = expert + p.proj_off1;  // up projection (FUSED only)
-  const float *x = p.x + (size_t)(inst / p.x_div) * p.x_stride;
   const size_t row_bytes = (size_t)p.chunks * T::kChunkBytes;
 
-  // chunk ownership and input slice
-  uint32_t chunk[CPL];
+  uint32_t lchunk[CPL];
   bool valid[CPL];
-  XSlice<FMT> xs[CPL];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
-    const uint32_t local = gl + (uint32_t)i * G;
-    chunk[i] = slice * p.chunks_per_slice + local;
-    valid[i] = local < p.chunks_per_slice && chunk[i] < p.chunks;
-    if (valid[i]) load_xslice<FMT>(x + (size_t)chunk[i] * 64, xs[i]);
-    else zero_xslice<FMT>(xs[i]);
+    lchunk[i] = gl + (uint32_t)i * G;
+    valid[i] = lchunk[i] < c_count;
   }
 
-  constexpr int kStreams = FUSED ? 2 : 1;
+  // input digits of the lane's chunk (register-resident when CPL == 1)
+  uint32_t xd[2 * kBlockDigitDwords];
+  float xsc[2];
+  auto fetch_x = [&](int i) {
+    if (valid[i]) {
+      const uint4 *d4 = reinterpret_cast<const uint4 *>(s_dig + (size_t)lchunk[i] * 2 * kBlockDigitDwords);
+#pragma unroll
+      for (int k = 0; k < 2 * kBlockDigitDwords / 4; ++k) {
+        const uint4 v = d4[k];
+        xd[4 * k] = v.x; xd[4 * k + 1] = v.y; xd[4 * k + 2] = v.z; xd[4 * k + 3] = v.w;
+      }
+      xsc[0] = s_scale[2 * lchunk[i]];
+      xsc[1] = s_scale[2 * lchunk[i] + 1];
+    } else {
+#pragma unroll
+      for (int k = 0; k < 2 * kBlockDigitDwords; ++k) xd[k] = 0u;
+      xsc[0] = xsc[1] = 0.f;
+    }
+  };
+  if constexpr (CPL == 1) fetch_x(0);
+
   for (uint32_t r0 = r_begin + grp * R; r0 < r_end; r0 += R * kGroups) {
     uint32_t wbuf[kStreams][CPL][R][T::kChunkDwords];
 #pragma unroll
@@ -98,32 +196,52 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjParams p) {
         for (int j = 0; j < R; ++j) {
           if (valid[i] && r0 + j < r_end) {
             const uint8_t *base = (sidx == 0 ? w0 : w1) + (size_t)(r0 + j) * row_bytes +
-                                  (size_t)chunk[i] * T::kChunkBytes;
+                                  (size_t)(c_begin + lchunk[i]) * T::kChunkBytes;
             load_chunk<FMT>(base, wbuf[sidx][i][j]);
           } else {
 #pragma unroll
-            for (int k = 0; k < T::kChunkDwords; ++k) wbuf[sidx][i][j][k] = 0x88888888u;
+            for (int k = 0; k < T::kChunkDwords; ++k) wbuf[sidx][i][j][k] = 0u;
           }
         }
     float acc[kStreams][R];
 #pragma unroll
     for (int sidx = 0; sidx < kStreams; ++sidx)
 #pragma unroll
-      for (int j = 0; j < R; ++j) {
-        float a = 0.f;
+      for (int j = 0; j < R; ++j) acc[sidx][j] = 0.f;
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) a += chunk_dot<FMT>(wbuf[sidx][i][j], xs[i]);
-        acc[sidx][j] = group_sum<G>(a);
-      }
+    for (int i = 0; i < CPL; ++i) {
+      if constexpr (CPL > 1) fetch_x(i);
+#pragma unroll
+      for (int sidx = 0; sidx < kStreams; ++sidx)
+#pragma unroll
+        for (int j = 0; j < R; ++j) acc[sidx][j] += chunk_idot<FMT>(wbuf[sidx][i][j], xd, xsc);
+    }
+#pragma unroll
+    for (int sidx = 0; sidx < kStreams; ++sidx)
+#pragma unroll
+      for (int j = 0; j < R; ++j) acc[sidx][j] = group_sum<G>(acc[sidx][j]);
     if (gl == 0) {
 #pragma unroll
       for (int j = 0; j < R; ++j) {
-        if (r0 + j < r_end) {
-          if constexpr (FUSED) out[r0 + j] = silu_mul(acc[0][j], acc[1][j]);
-          else out[r0 + j] = acc[0][j];
+        const uint32_t r = r0 + j;
+        if (r < r_end) {
+          if constexpr (FUSED) {
+            const float h = silu_mul(acc[0][j], acc[1][j]);
+            s_h[r - wg_r0] = h;
+            if (p.out) p.out[(size_t)inst * p.rows + r] = h;
+          } else {
+            p.out[((size_t)inst * p.slices + slice) * p.rows + r] = acc[0][j];
+          }
         }
       }
     }
+  }
+
+  if constexpr (FUSED) {
+    // 3. this workgroup's h rows -> digit planes for the down projection
+    __syncthreads();
+    const size_t b0 = (size_t)inst * p.hq_blocks + wg_r0 / 32;
+    pack_vector<FMT>(s_h, wg_rows / 32, p.hq_dig + b0 * kBlockDigitDwords, p.hq_scale + b0);
   }
 }
 
@@ -267,9 +385,9 @@ __global__ __launch_bounds__(256) void fill_kernel(uint64_t seed, uint64_t exper
 
 template <int FMT, int G, int CPL, int R, bool FUSED>
 static hipError_t launch_proj_t(const ProjParams &p, hipStream_t st) {
-  const uint32_t waves = p.n_inst * p.slices * p.waves_per_slice;
-  const uint32_t blocks = (waves + 3) / 4;
-  hipLaunchKernelGGL((proj_kernel<FMT, G, CPL, R, FUSED>), dim3(blocks), dim3(256), 0, st, p);
+  const uint32_t blocks = p.n_inst * p.slices * p.wgs_per_slice;
+  const size_t lds = proj_lds_bytes(p, FUSED);
+  hipLaunchKernelGGL((proj_kernel<FMT, G, CPL, R, FUSED>), dim3(blocks), dim3(256), lds, st, p);
   return hipGetLastError();
 }
 
@@ -277,13 +395,13 @@ template <int FMT, bool FUSED, int R>
 static hipError_t launch_proj_fmt(const ProjParams &p, int G, int CPL, hipStream_t st) {
   if (G == 16) return launch_proj_t<FMT, 16, 1, R, FUSED>(p, st);
   if (G == 32) return launch_proj_t<FMT, 32, 1, R, FUSED>(p, st);
-  // Two register-resident chunks per lane only fit the Q4_0 fused walk
-  // (max_fused_cpl); everything else streams one chunk per lane.
-  if constexpr (FUSED && FMT == FMT_Q4_0) {
-    if (CPL == 2) return launch_proj_t<FMT, 64, 2, R, FUSED>(p, st);
+  switch (CPL) {
+    case 1: return launch_proj_t<FMT, 64, 1, R, FUSED>(p, st);
+    case 2: return launch_proj_t<FMT, 64, 2, R, FUSED>(p, st);
+    case 3: return launch_proj_t<FMT, 64, 3, R, FUSED>(p, st);
+    case 4: return launch_proj_t<FMT, 64, 4, R, FUSED>(p, st);
+    default: return hipErrorInvalidValue;
   }
-  if (CPL != 1) return hipErrorInvalidValue;
-  return launch_proj_t<FMT, 64, 1, R, FUSED>(p, st);
 }
 
 hipError_t launch_proj(int fmt, bool fused, const ProjPlan &plan, const ProjParams &p, hipStream_t st) {
