@@ -167,12 +167,13 @@ def main() -> int:
     # Algorithmic bytes (packed weights of each distinct expert touched + f32
     # activations in/out).  Per launch of each stage (K experts per launch):
     proj = ebytes // 3
-    gate_up_bytes = K * 2 * proj + dm * 4 + K * dff * 4          # weights + x in + h out
-    down_bytes = K * proj + K * dff * 4 + K * 4 * dm * 4          # weights + h in + 4 column-slice partials
+    gate_up_bytes = K * 2 * proj + dm // 32 * 100 + K * dff // 32 * 100  # weights + x digits in + h digits out
+    down_bytes = K * proj + K * dff // 32 * 100 + K * 4 * dm * 4  # weights + h digits in + 4 slice partials
     combine_bytes = K * 4 * dm * 4 + 2 * dm * 4                   # partial slices + out read/write
     per_layer_bytes = K * ebytes + 3 * dm * 4  # + x_l in, out read + written
     token_bytes = L * per_layer_bytes
-    stage_bytes = {"gate_up": gate_up_bytes, "down": down_bytes, "combine": combine_bytes}
+    prep_bytes = dm * 4 + dm // 32 * 100 + K * 12                 # x in, digit planes out, slot pointers
+    stage_bytes = {"gate_up": gate_up_bytes, "down": down_bytes, "combine": combine_bytes, "prep": prep_bytes}
     stage_info = {}
     for name, (ms, cnt) in stages.items():
         if cnt:

@@ -102,11 +102,14 @@ int mer_hip_take_device_status(void);
 /* GPU stage timings (the StageTimings analogue, stage_timing.rs:6-29):
  * while enabled, each expert launch is bracketed by HIP events on its
  * stream.  read() synchronises the device and returns, per stage
- * {0 = gate/up + SiLU, 1 = down, 2 = combine}, the summed milliseconds and
- * launch counts since the last enable/read, then resets.  Timing must not
- * be enabled while the caller captures a HIP graph. */
+ * {0 = gate/up + SiLU, 1 = down, 2 = combine, 3 = input packing / expert
+ * resolution -- the flat-layout fallback's launches -- and 4 = the
+ * persistent decode kernel of the fast path}, the summed milliseconds and launch counts since the last
+ * enable/read, then resets.  Timing must not be enabled while the caller
+ * captures a HIP graph. */
+#define MER_STAGE_COUNT 5 /* 4 = the persistent decode kernel (fast path) */
 int mer_hip_stage_timing_enable(int enable);
-int mer_hip_stage_timing_read(double *ms /*[3]*/, uint64_t *counts /*[3]*/);
+int mer_hip_stage_timing_read(double *ms /*[MER_STAGE_COUNT]*/, uint64_t *counts /*[MER_STAGE_COUNT]*/);
 
 /* ---- host-only sizing and validation (no GPU work) ----------------- */
 /* expert_weight_bytes_for (inference.rs:1089-1146); saturates. */
@@ -172,6 +175,31 @@ int mer_hip_moe_forward(int dtype, size_t d_model, size_t d_ff,
                         const int32_t *d_expert_ids, const float *d_weights,
                         const float *d_x, float *d_out, unsigned flags,
                         void *stream);
+
+/* Per-layer arguments of mer_hip_moe_forward_layers (device pointers). */
+typedef struct mer_layer_args {
+  const void *const *expert_table; /* [table_len] expert blob pointers    */
+  size_t table_len;
+  const int32_t *expert_ids;       /* [n_tokens * top_k]                  */
+  const float *weights;            /* [n_tokens * top_k]                  */
+  const float *x;                  /* [n_tokens][d_model]; ignored for    */
+                                   /* layers > 0 under MER_MOE_CHAIN      */
+  float *out;                      /* [n_tokens][d_model]                 */
+} mer_layer_args;
+
+#define MER_MOE_CHAIN 4u /* layer l > 0 reads layer l-1's out as its x */
+
+/* n_layers (<= 64) routed-expert MoE layers of one decode step in a single
+ * persistent launch: the per-layer WeightedInto step of moe_step_inner
+ * (engine.rs:5548-5639) run for every layer of the model (model.rs:
+ * 2715-2741) without returning to the host.  Layers execute in order
+ * (layer l starts reading its input only after layer l-1 has written its
+ * output), with the same combine order and flags as mer_hip_moe_forward;
+ * under MER_MOE_CHAIN layer l's input is layer l-1's out.  Requires
+ * d_model and d_ff to be multiples of 64.  The launch occupies every CU;
+ * run nothing else on the device concurrently. */
+int mer_hip_moe_forward_layers(int dtype, size_t d_model, size_t d_ff, size_t n_layers, size_t n_tokens,
+                               size_t top_k, const mer_layer_args *layers, unsigned flags, void *stream);
 
 /* Synthetic bench / test data: fill n_blocks GGUF blocks of expert
  * `expert_index` starting at block `block_begin` with this library's

@@ -34,6 +34,7 @@ from .expert import (
     forward_q8_0_direct_into,
     init,
     moe_forward,
+    moe_forward_layers,
     q4_0_forward,
     q4_0_matvec,
     routed_expert_gpu_compatibility,

@@ -19,6 +19,17 @@ c_u64 = ctypes.c_uint64
 c_float = ctypes.c_float
 
 
+class MerLayerArgs(ctypes.Structure):
+    _fields_ = [
+        ("expert_table", c_void),
+        ("table_len", c_size),
+        ("expert_ids", c_void),
+        ("weights", c_void),
+        ("x", c_void),
+        ("out", c_void),
+    ]
+
+
 class MerErrorInfo(ctypes.Structure):
     _fields_ = [
         ("status", ctypes.c_int32),
@@ -73,6 +84,8 @@ SIGNATURES = {
     "mer_hip_moe_forward": (
         c_int, [c_int, c_size, c_size, c_size, c_size, c_void, c_size, c_void, c_void, c_void, c_void,
                 ctypes.c_uint, c_void]),
+    "mer_hip_moe_forward_layers": (
+        c_int, [c_int, c_size, c_size, c_size, c_size, c_size, ctypes.POINTER(MerLayerArgs), ctypes.c_uint, c_void]),
     "mer_hip_fill_synthetic": (
         c_int, [c_int, c_u64, c_u64, c_u64, c_u64, c_float, c_float, c_void, c_void]),
 }

@@ -65,9 +65,13 @@ int fmt_of(int dtype) { return dtype == MER_DTYPE_Q4_0 ? FMT_Q4_0 : FMT_Q8_0; }
 struct DeviceState {
   bool ready = false;
   int cus = 256;
-  uint32_t waves_per_cu = 12;
   float *scratch = nullptr;
   size_t scratch_floats = 0;
+  uint32_t *counters = nullptr;  // decode counters, all zero between launches
+  size_t counter_words = 0;
+  uint32_t *status = nullptr;
+  uint64_t clock_khz = 100000;
+  int occupancy[2][3][3] = {};   // resident decode workgroups per CU, by (fmt, GG, GD)
 };
 std::mutex g_mu;
 int g_device = -1;
@@ -76,7 +80,7 @@ DeviceState g_dev[64];
 // GPU stage timings (stage_timing.rs:6-29 analogue): when enabled, every
 // gate/up, down and combine launch is bracketed by a pair of events on the
 // launch stream; mer_hip_stage_timing_read sums their elapsed times.
-enum Stage { STAGE_GATE_UP = 0, STAGE_DOWN = 1, STAGE_COMBINE = 2, STAGE_COUNT = 3 };
+enum Stage { STAGE_GATE_UP = 0, STAGE_DOWN = 1, STAGE_COMBINE = 2, STAGE_PREP = 3, STAGE_DECODE = 4, STAGE_COUNT = 5 };
 struct TimedLaunch {
   hipEvent_t start, end;
   int stage;
@@ -138,34 +142,59 @@ int ensure_scratch(size_t floats, float **out) {
   return MER_OK;
 }
 
-// Choose the decomposition of one projection launch.  `waves_per_cu`
-// sets the grid size (default 12, MER_WAVES_PER_CU overrides at init).
-ProjPlan plan_projection(size_t rows, size_t cols, uint32_t n_inst, bool fused, bool aligned) {
+bool capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+// Decode counters live in their own allocation so they stay zero whatever
+// layout the scratch takes (the kernel re-zeroes what it used on exit).
+int ensure_counters(size_t words, hipStream_t st, uint32_t **out) {
+  DeviceState &d = g_dev[g_device];
+  words += 64;  // + exit counter
+  if (d.counter_words < words) {
+    if (capturing(st))
+      return fail(MER_ERR_PHYSICAL_CAPACITY, "decode counters must grow, which cannot happen under graph capture: "
+                                             "run the same call once before capturing");
+    if (d.counters) {
+      hipError_t e = hipDeviceSynchronize();
+      if (e != hipSuccess) return hip_fail(e, MER_ERR_DEVICE_LOST, "synchronise before counter growth");
+      (void)hipFree(d.counters);
+      d.counters = nullptr;
+      d.counter_words = 0;
+    }
+    size_t want = words < (1u << 16) ? (1u << 16) : words;
+    hipError_t e = hipMalloc(&d.counters, want * 4);
+    if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "decode counter allocation");
+    e = hipMemset(d.counters, 0, want * 4);
+    if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "decode counter initialisation");
+    d.counter_words = want;
+  }
+  *out = d.counters;
+  return MER_OK;
+}
+
+int g_index(int g) { return g == 16 ? 0 : (g == 32 ? 1 : 2); }
+
+// Choose the decomposition of one projection launch.
+ProjPlan plan_projection(size_t rows, size_t cols, bool fused, bool aligned) {
   ProjPlan pl{};
   // Fast path: rows of an even number of blocks (4-byte aligned chunks) and
-  // 32-row blocks of h; every configuration of the benchmark qualifies.
+  // whole 32-row tiles; every configuration of the benchmark qualifies.
   pl.fast = aligned && cols % 64 == 0 && rows % 64 == 0 && cols <= MER_MAX_EXPERT_DIM &&
             rows <= MER_MAX_EXPERT_DIM && rows > 0;
   if (!pl.fast) return pl;
   const uint32_t C = (uint32_t)(cols / 64);
   if (C <= 16) { pl.G = 16; pl.CPL = 1; pl.slices = 1; }
   else if (C <= 32) { pl.G = 32; pl.CPL = 1; pl.slices = 1; }
-  else if (fused) { pl.G = 64; pl.CPL = (int)div_ceil(C, 64); pl.slices = 1; }
-  else { pl.G = 64; pl.CPL = 1; pl.slices = (uint32_t)div_ceil(C, 64); }
+  else if (fused) {
+    pl.G = 64;
+    pl.CPL = (int)div_ceil(C, 64);
+    pl.slices = 1;
+    if (pl.CPL > kMaxCpl) pl.fast = false;
+  } else { pl.G = 64; pl.CPL = 1; pl.slices = (uint32_t)div_ceil(C, 64); }
   pl.chunks_per_slice = (uint32_t)div_ceil(C, pl.slices);
-  const uint32_t R = fused ? kFusedRows : kDownRows;
-  // rows of a wave: whole passes of all lane groups, and (gate/up) whole
-  // 32-row blocks of h per 4-wave workgroup
-  uint32_t unit = R * (64u / (uint32_t)pl.G);
-  while (unit % 8) unit *= 2;
-  const uint64_t target_waves = (uint64_t)g_dev[g_device].cus * g_dev[g_device].waves_per_cu;
-  const uint64_t per_slice = (uint64_t)n_inst * pl.slices;
-  uint64_t want = target_waves / per_slice;
-  if (want < 4) want = 4;
-  uint64_t rpw = div_ceil(rows, want);
-  rpw = div_ceil(rpw, unit) * unit;
-  pl.rows_per_wave = (uint32_t)rpw;
-  pl.wgs_per_slice = (uint32_t)div_ceil(rows, 4 * rpw);
+  pl.tiles = (uint32_t)(rows / kTileRows);
   return pl;
 }
 
@@ -207,7 +236,130 @@ int validate(int dtype, size_t len, size_t x_len, size_t y_len, size_t dm, size_
   return fail(MER_ERR_UNSUPPORTED_DTYPE, "unsupported expert dtype %d (only Q4_0=4 and Q8_0=5)", dtype);
 }
 
-// Enqueue gate/up -> down -> combine for n_inst expert instances.
+// Geometry of one projection for the decode kernel: lane-group width G,
+// column slices of at most 64 chunks, chunks per slice.
+struct SliceGeom {
+  int G;
+  uint32_t slices, cps;
+};
+SliceGeom slice_geom(uint32_t chunks) {
+  SliceGeom g{};
+  g.slices = (uint32_t)div_ceil(chunks, 64);
+  g.cps = (uint32_t)div_ceil(chunks, g.slices);
+  g.G = g.cps <= 16 ? 16 : (g.cps <= 32 ? 32 : 64);
+  return g;
+}
+
+bool decode_eligible(size_t dm, size_t dff, const uint8_t *single) {
+  if (single && ((uintptr_t)single % 4) != 0) return false;
+  return dm % 64 == 0 && dff % 64 == 0 && dm > 0 && dff > 0 && dm <= MER_MAX_EXPERT_DIM && dff <= MER_MAX_EXPERT_DIM;
+}
+
+// One persistent launch for n_layers MoE layers (fast path).
+int run_decode(int dtype, size_t dm, size_t dff, uint32_t n_layers, uint32_t n_tok, uint32_t top_k,
+               const LayerArgs *layers, const uint8_t *single, unsigned flags, hipStream_t st) {
+  DeviceState &dev = g_dev[g_device];
+  const int fmt = fmt_of(dtype);
+  DecodeParams p{};
+  for (uint32_t l = 0; l < n_layers; ++l) p.layers[l] = layers[l];
+  p.single = single;
+  p.n_layers = n_layers;
+  p.n_tok = n_tok;
+  p.top_k = top_k;
+  p.n_inst = n_tok * top_k;
+  p.d_model = (uint32_t)dm;
+  p.d_ff = (uint32_t)dff;
+  p.flags = flags;
+  p.proj_bytes = div_ceil(dm * dff, 32) * block_bytes(dtype);
+  p.xblocks = (uint32_t)(dm / 32);
+  p.hblocks = (uint32_t)(dff / 32);
+  const SliceGeom gg = slice_geom((uint32_t)(dm / 64));
+  const SliceGeom gd = slice_geom((uint32_t)(dff / 64));
+  p.g_chunks = (uint32_t)(dm / 64);
+  p.g_slices = gg.slices;
+  p.g_cps = gg.cps;
+  p.g_tiles = (uint32_t)(dff / kTileRows);
+  p.d_chunks = (uint32_t)(dff / 64);
+  p.d_slices = gd.slices;
+  p.d_cps = gd.cps;
+  p.d_tiles = (uint32_t)(dm / kTileRows);
+  const uint32_t pack_blocks = fmt == FMT_Q4_0 ? 16 : 8;
+  p.p_items = (uint32_t)div_ceil(p.xblocks, pack_blocks);
+  p.off_p = n_tok;
+  p.off_g = p.off_p + n_tok * p.p_items;
+  p.off_d = p.off_g + p.n_inst * p.g_slices * p.g_tiles;
+  p.items_per_layer = p.off_d + p.n_inst * p.d_slices * p.d_tiles;
+  p.total_items = (uint64_t)p.items_per_layer * n_layers;
+
+  // counters per layer: R[n_tok] P[n_tok] G-arrive[n_inst*g_tiles] G-done[n_inst*d_slices]
+  //                     D-arrive[n_tok*d_tiles] C-done[n_tok]
+  p.c_r = 0;
+  p.c_p = p.c_r + n_tok;
+  p.c_ga = p.c_p + n_tok;
+  p.c_gd = p.c_ga + p.n_inst * p.g_tiles;
+  p.c_da = p.c_gd + p.n_inst * p.d_slices;
+  p.c_c = p.c_da + n_tok * p.d_tiles;
+  p.cnt_per_layer = p.c_c + n_tok;
+  p.n_counters = p.cnt_per_layer * n_layers;
+
+  auto up64 = [](size_t v) { return (v + 63) / 64 * 64; };
+  const size_t L = n_layers;
+  const size_t n_ptr = up64(L * p.n_inst * 2);
+  const size_t n_xd = up64(L * n_tok * p.xblocks * kBlockDigitDwords);
+  const size_t n_xs = up64(L * n_tok * p.xblocks);
+  const size_t n_gp = p.g_slices > 1 ? up64(L * p.n_inst * p.g_slices * 2 * dff) : 0;
+  const size_t n_hd = up64(L * p.n_inst * p.hblocks * kBlockDigitDwords);
+  const size_t n_hs = up64(L * p.n_inst * p.hblocks);
+  const size_t n_pa = up64(L * p.n_inst * p.d_slices * dm);
+  float *scratch = nullptr;
+  if (dev.scratch_floats < n_ptr + n_xd + n_xs + n_gp + n_hd + n_hs + n_pa && capturing(st))
+    return fail(MER_ERR_PHYSICAL_CAPACITY,
+                "scratch must grow, which cannot happen under graph capture: run the same call once before capturing");
+  int rc = ensure_scratch(n_ptr + n_xd + n_xs + n_gp + n_hd + n_hs + n_pa, &scratch);
+  if (rc) return rc;
+  float *cur = scratch;
+  p.inst_ptr = reinterpret_cast<const uint8_t **>(cur);
+  cur += n_ptr;
+  p.xq_dig = reinterpret_cast<uint32_t *>(cur);
+  cur += n_xd;
+  p.xq_scale = cur;
+  cur += n_xs;
+  p.gpart = cur;
+  cur += n_gp;
+  p.hq_dig = reinterpret_cast<uint32_t *>(cur);
+  cur += n_hd;
+  p.hq_scale = cur;
+  cur += n_hs;
+  p.partial = cur;
+  uint32_t *counters = nullptr;
+  if ((rc = ensure_counters(p.n_counters, st, &counters))) return rc;
+  p.counters = counters;
+  p.exit_count = counters + dev.counter_words - 1;
+  p.abort_flag = counters + dev.counter_words - 2;
+  p.status = dev.status;
+  p.timeout_ticks = dev.clock_khz * 2000;  // 2 s per wait
+
+  const void *fn = decode_kernel_fn(fmt, gg.G, gd.G);
+  int &occ = dev.occupancy[fmt][g_index(gg.G)][g_index(gd.G)];
+  if (occ == 0) {
+    int n = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, 64, 0);
+    if (e != hipSuccess || n <= 0) return hip_fail(e, MER_ERR_RUNTIME_INVARIANT, "decode kernel occupancy query");
+    occ = n;
+  }
+  uint64_t grid = (uint64_t)dev.cus * (uint64_t)occ;
+  if (grid > p.total_items) grid = p.total_items;
+  if (grid == 0) return MER_OK;
+
+  TimedLaunch *tl = nullptr;
+  int trc = timing_begin(STAGE_DECODE, st, &tl);
+  if (trc) return trc;
+  hipError_t e = launch_decode(fn, (uint32_t)grid, p, st);
+  if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "decode launch");
+  return timing_end(tl, st);
+}
+
+// Enqueue prep -> gate/up -> down -> combine for n_inst expert instances.
 int run_experts(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t top_k, const void *const *table,
                 uint32_t table_len, const int32_t *ids, const uint8_t *single, const float *weights,
                 const float *x, float *out, unsigned flags, hipStream_t st, bool direct_out) {
@@ -215,89 +367,146 @@ int run_experts(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
   const uint32_t n_inst = n_tokens * top_k;
   const size_t proj = div_ceil(dm * dff, 32) * block_bytes(dtype);
   const bool aligned = single ? ((uintptr_t)single % 4 == 0) : true;
+  if (decode_eligible(dm, dff, single)) {
+    LayerArgs la{};
+    la.table = table;
+    la.table_len = table_len;
+    la.ids = ids;
+    la.weights = weights;
+    la.x = x;
+    la.out = out;
+    return run_decode(dtype, dm, dff, 1, n_tokens, top_k, &la, single, flags, st);
+  }
 
-  ProjPlan pg = plan_projection(dff, dm, n_inst, true, aligned);
-  ProjPlan pd = plan_projection(dm, dff, n_inst, false, aligned);
+  const ProjPlan pg = plan_projection(dff, dm, true, aligned);
+  const ProjPlan pd = plan_projection(dm, dff, false, aligned);
   const bool fast = pg.fast && pd.fast;
   const uint32_t slices = fast ? pd.slices : 1;
-
   const bool write_direct = direct_out && slices == 1 && n_inst == 1 && flags == 0;
-  // scratch: f32 h (generic path) | h digit planes + scales (fast path) | partials
-  const size_t hblocks = dff / 32;
-  const size_t h_floats = fast ? 0 : (size_t)n_inst * dff;
-  const size_t hq_dwords = fast ? (size_t)n_inst * hblocks * kBlockDigitDwords : 0;
-  const size_t hs_floats = fast ? (size_t)n_inst * hblocks : 0;
-  const size_t p_floats = write_direct ? 0 : (size_t)n_inst * slices * dm;
+
+  // scratch (floats; every region 256-byte aligned):
+  //   inst_ptr | x digits + scales | h digits + scales (fast) or f32 h | partials
   auto up64 = [](size_t v) { return (v + 63) / 64 * 64; };
+  const size_t xblocks = dm / 32, hblocks = dff / 32;
+  const size_t n_ptr = up64(2 * (size_t)n_inst);
+  const size_t n_xd = fast ? up64((size_t)n_tokens * xblocks * kBlockDigitDwords) : 0;
+  const size_t n_xs = fast ? up64((size_t)n_tokens * xblocks) : 0;
+  const size_t n_hd = fast ? up64((size_t)n_inst * hblocks * kBlockDigitDwords) : 0;
+  const size_t n_hs = fast ? up64((size_t)n_inst * hblocks) : 0;
+  const size_t n_h = fast ? 0 : up64((size_t)n_inst * dff);
+  const size_t n_p = write_direct ? 0 : up64((size_t)n_inst * slices * dm);
   float *scratch = nullptr;
-  int rc = ensure_scratch(up64(h_floats) + up64(hq_dwords) + up64(hs_floats) + up64(p_floats), &scratch);
+  int rc = ensure_scratch(n_ptr + n_xd + n_xs + n_hd + n_hs + n_h + n_p, &scratch);
   if (rc) return rc;
-  float *h = scratch;
-  uint32_t *hq_dig = reinterpret_cast<uint32_t *>(scratch + up64(h_floats));
-  float *hq_scale = scratch + up64(h_floats) + up64(hq_dwords);
-  float *partial = write_direct ? out : hq_scale + up64(hs_floats);
+  float *cur = scratch;
+  const uint8_t **inst_ptr = reinterpret_cast<const uint8_t **>(cur);
+  cur += n_ptr;
+  uint32_t *xq_dig = reinterpret_cast<uint32_t *>(cur);
+  cur += n_xd;
+  float *xq_scale = cur;
+  cur += n_xs;
+  uint32_t *hq_dig = reinterpret_cast<uint32_t *>(cur);
+  cur += n_hd;
+  float *hq_scale = cur;
+  cur += n_hs;
+  float *h = cur;
+  cur += n_h;
+  float *partial = write_direct ? out : cur;
 
-  ProjParams p{};
-  p.table = table;
-  p.table_len = table_len;
-  p.ids = ids;
-  p.single = single;
-  p.n_inst = n_inst;
-
-  // gate/up + SiLU -> h (digit planes on the fast path)
-  p.proj_off0 = 0;
-  p.proj_off1 = proj;
-  p.rows = (uint32_t)dff;
-  p.chunks = (uint32_t)(dm / 64);
-  p.x = x;
-  p.x_div = top_k;
-  p.x_stride = dm;
-  p.hq_dig = hq_dig;
-  p.hq_scale = hq_scale;
-  p.hq_blocks = (uint32_t)hblocks;
   hipError_t e;
   TimedLaunch *tl = nullptr;
-  int trc = timing_begin(STAGE_GATE_UP, st, &tl);
-  if (trc) return trc;
+  int trc;
+
+  PrepParams q{};
+  q.table = table;
+  q.table_len = table_len;
+  q.ids = ids;
+  q.single = single;
+  q.top_k = top_k;
+  q.inst_ptr = inst_ptr;
+  q.x = x;
+  q.d_model = (uint32_t)dm;
+  q.blocks = (uint32_t)xblocks;
+  q.xq_dig = fast ? xq_dig : nullptr;
+  q.xq_scale = xq_scale;
+  if ((trc = timing_begin(STAGE_PREP, st, &tl))) return trc;
+  e = launch_prep(fmt, q, n_tokens, st);
+  if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "prep launch");
+  if ((trc = timing_end(tl, st))) return trc;
+
+  // gate/up + SiLU -> h (digit planes on the fast path)
+  if ((trc = timing_begin(STAGE_GATE_UP, st, &tl))) return trc;
   if (fast) {
-    p.out = nullptr;
+    ProjParams p{};
+    p.inst_ptr = inst_ptr;
+    p.n_inst = n_inst;
+    p.proj_off0 = 0;
+    p.proj_off1 = proj;
+    p.rows = (uint32_t)dff;
+    p.chunks = (uint32_t)(dm / 64);
     p.slices = 1;
     p.chunks_per_slice = pg.chunks_per_slice;
-    p.wgs_per_slice = pg.wgs_per_slice;
-    p.rows_per_wave = pg.rows_per_wave;
-    p.lds_blocks = 2 * pg.chunks_per_slice;
+    p.tiles = pg.tiles;
+    p.xq_dig = xq_dig;
+    p.xq_scale = xq_scale;
+    p.xq_blocks = (uint32_t)xblocks;
+    p.x_div = top_k;
+    p.hq_dig = hq_dig;
+    p.hq_scale = hq_scale;
+    p.hq_blocks = (uint32_t)hblocks;
+    p.out = nullptr;
     e = launch_proj(fmt, true, pg, p, st);
   } else {
-    p.out = h;
-    p.slices = 1;
-    e = launch_generic(fmt, true, p, (uint32_t)dm, st);
+    GenericParams g{};
+    g.inst_ptr = inst_ptr;
+    g.n_inst = n_inst;
+    g.proj_off0 = 0;
+    g.proj_off1 = proj;
+    g.rows = (uint32_t)dff;
+    g.cols = (uint32_t)dm;
+    g.fused = 1;
+    g.x = x;
+    g.x_div = top_k;
+    g.x_stride = dm;
+    g.out = h;
+    e = launch_generic(fmt, g, st);
   }
   if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "gate/up launch");
   if ((trc = timing_end(tl, st))) return trc;
 
   // down -> partial [inst][slice][dm]
-  p.proj_off0 = 2 * proj;
-  p.proj_off1 = 0;
-  p.rows = (uint32_t)dm;
-  p.chunks = (uint32_t)(dff / 64);
-  p.x = h;
-  p.x_div = 1;
-  p.x_stride = dff;
-  p.xq_dig = hq_dig;
-  p.xq_scale = hq_scale;
-  p.xq_blocks = (uint32_t)hblocks;
-  p.out = partial;
   if ((trc = timing_begin(STAGE_DOWN, st, &tl))) return trc;
   if (fast) {
+    ProjParams p{};
+    p.inst_ptr = inst_ptr;
+    p.n_inst = n_inst;
+    p.proj_off0 = 2 * proj;
+    p.proj_off1 = 0;
+    p.rows = (uint32_t)dm;
+    p.chunks = (uint32_t)(dff / 64);
     p.slices = pd.slices;
     p.chunks_per_slice = pd.chunks_per_slice;
-    p.wgs_per_slice = pd.wgs_per_slice;
-    p.rows_per_wave = pd.rows_per_wave;
-    p.lds_blocks = 2 * pd.chunks_per_slice;
+    p.tiles = pd.tiles;
+    p.xq_dig = hq_dig;
+    p.xq_scale = hq_scale;
+    p.xq_blocks = (uint32_t)hblocks;
+    p.x_div = 1;
+    p.out = partial;
     e = launch_proj(fmt, false, pd, p, st);
   } else {
-    p.slices = 1;
-    e = launch_generic(fmt, false, p, (uint32_t)dff, st);
+    GenericParams g{};
+    g.inst_ptr = inst_ptr;
+    g.n_inst = n_inst;
+    g.proj_off0 = 2 * proj;
+    g.proj_off1 = 0;
+    g.rows = (uint32_t)dm;
+    g.cols = (uint32_t)dff;
+    g.fused = 0;
+    g.x = h;
+    g.x_div = 1;
+    g.x_stride = dff;
+    g.out = partial;
+    e = launch_generic(fmt, g, st);
   }
   if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "down launch");
   if ((trc = timing_end(tl, st))) return trc;
@@ -340,10 +549,11 @@ int mer_hip_init(int device) {
   e = hipSetDevice(device);
   if (e != hipSuccess) return hip_fail(e, MER_ERR_DEVICE_LOST, "hipSetDevice");
   g_dev[device].cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
-  if (const char *w = getenv("MER_WAVES_PER_CU")) {
-    const long v = strtol(w, nullptr, 10);
-    if (v >= 1 && v <= 64) g_dev[device].waves_per_cu = (uint32_t)v;
-  }
+  int khz = 0;
+  if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device) == hipSuccess && khz > 0)
+    g_dev[device].clock_khz = (uint64_t)khz;
+  g_dev[device].status = device_status_ptr();
+  if (!g_dev[device].status) return fail(MER_ERR_RUNTIME_INVARIANT, "device status symbol not found");
   g_dev[device].ready = true;
   g_device = device;
   return ok();
@@ -355,6 +565,7 @@ int mer_hip_shutdown(void) {
   DeviceState &d = g_dev[g_device];
   (void)hipDeviceSynchronize();
   if (d.scratch) (void)hipFree(d.scratch);
+  if (d.counters) (void)hipFree(d.counters);
   d = DeviceState{};
   g_device = -1;
   return MER_OK;
@@ -528,15 +739,49 @@ int mer_hip_moe_forward(int dtype, size_t d_model, size_t d_ff, size_t n_tokens,
   rc = mer_routed_expert_gpu_compatibility(dtype, d_model, d_ff);
   if (rc) return rc;
   if (d_model == 0 || d_ff == 0) return fail(MER_ERR_INVALID_LAYOUT, "expert dimensions must be non-zero");
-  if (flags & ~3u) return fail(MER_ERR_INVALID_LAYOUT, "unknown flags 0x%x", flags);
+  if (flags & ~3u) return fail(MER_ERR_INVALID_LAYOUT, "unknown flags 0x%x (CHAIN applies to mer_hip_moe_forward_layers)", flags);
   if ((flags & 3u) == 3u) return fail(MER_ERR_INVALID_LAYOUT, "RESIDUAL and ACCUMULATE are exclusive");
   if (n_tokens == 0 || top_k == 0) return MER_OK;
-  if (n_tokens * top_k > (1u << 24) || table_len > UINT32_MAX)
+  if (n_tokens * top_k > (1u << 16) || table_len > UINT32_MAX)
     return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "too many expert instances");
   if (!d_expert_table || !d_expert_ids || !d_weights || !d_x || !d_out)
     return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
   return run_experts(dtype, d_model, d_ff, (uint32_t)n_tokens, (uint32_t)top_k, d_expert_table, (uint32_t)table_len,
                      d_expert_ids, nullptr, d_weights, d_x, d_out, flags, (hipStream_t)stream, false);
+}
+
+int mer_hip_moe_forward_layers(int dtype, size_t d_model, size_t d_ff, size_t n_layers, size_t n_tokens,
+                               size_t top_k, const mer_layer_args *layers, unsigned flags, void *stream) {
+  int rc = require_init();
+  if (rc) return rc;
+  if (dtype != MER_DTYPE_Q4_0 && dtype != MER_DTYPE_Q8_0)
+    return fail(MER_ERR_UNSUPPORTED_DTYPE, "unsupported expert dtype %d", dtype);
+  rc = mer_routed_expert_gpu_compatibility(dtype, d_model, d_ff);
+  if (rc) return rc;
+  if (flags & ~(MER_MOE_RESIDUAL | MER_MOE_ACCUMULATE | MER_MOE_CHAIN))
+    return fail(MER_ERR_INVALID_LAYOUT, "unknown flags 0x%x", flags);
+  if ((flags & 3u) == 3u) return fail(MER_ERR_INVALID_LAYOUT, "RESIDUAL and ACCUMULATE are exclusive");
+  if (n_layers == 0 || n_tokens == 0 || top_k == 0) return MER_OK;
+  if (n_layers > kMaxLayers) return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "at most %u layers per call", kMaxLayers);
+  if (!decode_eligible(d_model, d_ff, nullptr))
+    return fail(MER_ERR_INVALID_LAYOUT,
+                "multi-layer decode needs d_model and d_ff multiples of 64 (single-layer calls accept any shape)");
+  if (n_tokens * top_k > (1u << 16) || !layers) return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "too many expert instances");
+  LayerArgs la[kMaxLayers];
+  for (size_t l = 0; l < n_layers; ++l) {
+    const mer_layer_args &a = layers[l];
+    if (!a.expert_table || !a.expert_ids || !a.weights || !a.out || (!a.x && (l == 0 || !(flags & MER_MOE_CHAIN))))
+      return fail(MER_ERR_INVALID_LAYOUT, "layer %zu: null device pointer", l);
+    if (a.table_len > UINT32_MAX) return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "table too large");
+    la[l].table = a.expert_table;
+    la[l].table_len = (uint32_t)a.table_len;
+    la[l].ids = a.expert_ids;
+    la[l].weights = a.weights;
+    la[l].x = a.x;
+    la[l].out = a.out;
+  }
+  return run_decode(dtype, d_model, d_ff, (uint32_t)n_layers, (uint32_t)n_tokens, (uint32_t)top_k, la, nullptr,
+                    flags, (hipStream_t)stream);
 }
 
 int mer_hip_fill_synthetic(int dtype, uint64_t seed, uint64_t expert_index, uint64_t block_begin, uint64_t n_blocks,

@@ -9,51 +9,65 @@
 
 namespace mer {
 
-// Rows per pass of one lane group: the fused gate/up walk streams 2 rows
-// of each projection per pass (4 chunks in flight per lane), the down walk
-// streams 4 rows.
-constexpr int kFusedRows = 2;
-constexpr int kDownRows = 4;
-// Chunks a lane walks per row (G = 64); inputs beyond one chunk are read
-// from LDS per pass.
+// A projection workgroup owns a tile of 32 output rows (one block of h for
+// the gate/up kernel), 8 rows per wave.
+constexpr uint32_t kRowsPerWave = 8;
+constexpr uint32_t kTileRows = 4 * kRowsPerWave;
 constexpr int kMaxCpl = 4;
+
+// prep_kernel: pack x per token, resolve one blob pointer per expert slot.
+struct PrepParams {
+  const void *const *table;  // expert table (device), or null with `single`
+  uint32_t table_len;
+  const int32_t *ids;        // [n_tokens * top_k]
+  const uint8_t *single;     // single expert blob (overrides table / ids)
+  uint32_t top_k;
+  const uint8_t **inst_ptr;  // out: [n_tokens * top_k]
+  const float *x;            // [n_tokens][d_model]
+  uint32_t d_model;
+  uint32_t blocks;           // d_model / 32
+  uint32_t *xq_dig;          // out (fast path): [n_tokens][blocks][24], or null
+  float *xq_scale;           // out: [n_tokens][blocks]
+};
 
 // Arguments of one projection launch (passed by value).
 struct ProjParams {
-  const void *const *table;  // expert table (device), or null with `single`
-  uint32_t table_len;
-  const int32_t *ids;        // instance -> expert id (device)
-  const uint8_t *single;     // single expert blob (device), overrides table
-  uint32_t n_inst;           // expert instances (token x slot)
+  const uint8_t *const *inst_ptr;  // blob per expert instance (null = miss)
+  uint32_t n_inst;
   size_t proj_off0;          // byte offset of the (gate | down) projection
   size_t proj_off1;          // byte offset of the up projection (fused)
   uint32_t rows;             // output rows of the projection
   uint32_t chunks;           // 64-weight chunks per row
   uint32_t slices;           // column slices
   uint32_t chunks_per_slice;
-  uint32_t wgs_per_slice;    // workgroups walking one (instance, slice)
-  uint32_t rows_per_wave;    // rows of one wave (a workgroup owns 4x)
-  uint32_t lds_blocks;       // input blocks staged in LDS per workgroup
-  const float *x;            // f32 input vectors (gate/up; generic kernel)
-  uint32_t x_div;            // input index = instance / x_div
-  size_t x_stride;           // floats between consecutive inputs
-  const uint32_t *xq_dig;    // packed inputs of the down projection
-  const float *xq_scale;     //   [n_inst][xq_blocks] digit planes / scales
+  uint32_t tiles;            // 32-row tiles per (instance, slice)
+  const uint32_t *xq_dig;    // packed input vectors [.][xq_blocks][24]
+  const float *xq_scale;     //   and their block scales
   uint32_t xq_blocks;
-  uint32_t *hq_dig;          // packed h written by the gate/up kernel
-  float *hq_scale;           //   [n_inst][hq_blocks]
+  uint32_t x_div;            // input index = instance / x_div
+  uint32_t *hq_dig;          // gate/up: packed h [n_inst][hq_blocks][24]
+  float *hq_scale;
   uint32_t hq_blocks;
   float *out;                // down: [n_inst][slices][rows]; gate/up: f32 h or null
 };
 
-inline size_t proj_lds_bytes(const ProjParams &p, bool fused) {
-  return (size_t)p.lds_blocks * (kBlockDigitDwords * 4 + 4) + (fused ? (size_t)4 * p.rows_per_wave * 4 : 0);
-}
+// Flat-layout fallback (any shape): f32 inputs and outputs.
+struct GenericParams {
+  const uint8_t *const *inst_ptr;
+  uint32_t n_inst;
+  size_t proj_off0, proj_off1;
+  uint32_t rows, cols;
+  int fused;
+  const float *x;
+  uint32_t x_div;
+  size_t x_stride;
+  float *out;  // [n_inst][rows]
+};
 
 struct ProjPlan {
   bool fast;
   int G, CPL;
-  uint32_t slices, chunks_per_slice, wgs_per_slice, rows_per_wave;
+  uint32_t slices, chunks_per_slice, tiles;
 };
 
 struct CombineParams {
@@ -65,8 +79,57 @@ struct CombineParams {
   uint32_t flags;
 };
 
+// ---- persistent decode kernel (mer_decode.hip) -------------------------
+constexpr uint32_t kFlagResidual = 1u;    // out = x + sum_i w_i y_i
+constexpr uint32_t kFlagAccumulate = 2u;  // out += sum_i w_i y_i
+constexpr uint32_t kFlagChain = 4u;       // layer l > 0 reads layer l-1's out
+constexpr uint32_t kMaxLayers = 64;
+
+struct LayerArgs {
+  const void *const *table;  // device array of expert blob pointers
+  uint32_t table_len;
+  const int32_t *ids;        // [n_tok * top_k]
+  const float *weights;      // [n_tok * top_k] or null (weight 1, no skip)
+  const float *x;            // [n_tok][d_model] (layer 0, or every layer without chaining)
+  float *out;                // [n_tok][d_model]
+};
+
+struct DecodeParams {
+  LayerArgs layers[kMaxLayers];
+  const uint8_t *single;     // single-expert mode: this blob for every slot
+  uint32_t n_layers, n_tok, top_k, n_inst;
+  uint32_t d_model, d_ff, flags;
+  size_t proj_bytes;         // bytes of one projection
+  uint32_t xblocks, hblocks; // d_model / 32, d_ff / 32
+  uint32_t g_chunks, g_slices, g_cps, g_tiles;  // gate/up: chunks per row, slices, chunks per slice, tiles
+  uint32_t d_chunks, d_slices, d_cps, d_tiles;  // down
+  uint32_t p_items;          // packing items per token
+  uint32_t items_per_layer, off_p, off_g, off_d;
+  uint64_t total_items;
+  // scratch, all [layer]-major
+  const uint8_t **inst_ptr;  // [L][n_inst]
+  uint32_t *xq_dig;          // [L][n_tok][xblocks][24]
+  float *xq_scale;           // [L][n_tok][xblocks]
+  float *gpart;              // [L][n_inst][g_slices][2][d_ff]  (g_slices > 1)
+  uint32_t *hq_dig;          // [L][n_inst][hblocks][24]
+  float *hq_scale;           // [L][n_inst][hblocks]
+  float *partial;            // [L][n_inst][d_slices][d_model]
+  uint32_t *counters;        // [L][cnt_per_layer], zero between launches
+  uint32_t cnt_per_layer, c_r, c_p, c_ga, c_gd, c_da, c_c;
+  uint32_t n_counters;
+  uint32_t *exit_count;
+  uint32_t *abort_flag;      // set by a timed-out wait; later waits give up
+  uint32_t *status;
+  uint64_t timeout_ticks;
+};
+
+const void *decode_kernel_fn(int fmt, int gg, int gd);
+hipError_t launch_decode(const void *fn, uint32_t grid, const DecodeParams &p, hipStream_t st);
+uint32_t *device_status_ptr();
+
+hipError_t launch_prep(int fmt, const PrepParams &q, uint32_t n_tokens, hipStream_t st);
 hipError_t launch_proj(int fmt, bool fused, const ProjPlan &plan, const ProjParams &p, hipStream_t st);
-hipError_t launch_generic(int fmt, bool fused, const ProjParams &p, uint32_t cols, hipStream_t st);
+hipError_t launch_generic(int fmt, const GenericParams &p, hipStream_t st);
 hipError_t launch_combine(const CombineParams &c, hipStream_t st);
 hipError_t launch_dequant(int fmt, const uint8_t *src, size_t n_weights, float *dst, hipStream_t st);
 hipError_t launch_q4_raw(const uint8_t *w, size_t w_block_off, uint32_t rows, uint32_t bpr,

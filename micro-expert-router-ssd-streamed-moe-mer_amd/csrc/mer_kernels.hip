@@ -2,21 +2,24 @@
 //
 // Hot path (reference inference.rs:3291-3306 / :3636-3746, the expert math
 // behind engine.rs:1761-1848 and the combine of engine.rs:5548-5639):
-//   h_i = silu(W_gate,i x) * (W_up,i x)          proj_kernel<.., FUSED=true>
-//   p_i = W_down,i h_i  (split over column slices) proj_kernel<.., FUSED=false>
-//   out = [x +] sum_i w_i p_i                     combine_kernel
+//   prep_kernel          x -> block fixed-point digit planes (once per
+//                        token); expert id -> blob pointer (once per slot)
+//   proj_kernel<FUSED>   h_i = silu(W_gate,i x) * (W_up,i x), written as
+//                        digit planes for the down projection
+//   proj_kernel<!FUSED>  p_i = W_down,i h_i over column slices
+//   combine_kernel       out = [x +] sum_i w_i p_i
 //
 // Decomposition of proj_kernel.  A workgroup (4 waves) owns one (expert
-// instance, column slice, row range).  It first brings its slice of the
-// input vector into LDS as block fixed-point digit planes (quantising x
-// itself in the gate/up kernel; copying the h planes the gate/up kernel
-// produced in the down kernel).  A wave64 is cut into 64/G lane groups of G
-// lanes (G = 16, 32 or 64); a lane group owns G*CPL consecutive 64-weight
-// chunks of the slice and walks down the wave's rows, R rows per pass,
-// streaming each weight byte from HBM exactly once with 16-byte loads and
-// consuming it with packed integer dot instructions.  Row sums are reduced
-// across the G lanes with shuffles.  The gate/up kernel finally packs its
-// rows of h = silu(g) * u into digit planes for the down kernel.
+// instance, column slice, 32-row tile); each wave owns 8 rows of the tile.
+// A wave64 is cut into 64/G lane groups of G lanes (G = 16, 32 or 64); a
+// lane group owns G*CPL consecutive 64-weight chunks of the slice and walks
+// its rows R at a time.  Each weight byte is streamed from HBM exactly once
+// with 16-byte loads and consumed by packed integer dot instructions; the
+// loads of the next pass are in flight while a pass is computed, and the
+// first pass is issued before the input digits are fetched, so no
+// prologue latency sits in front of the weight stream.  Row sums are
+// reduced across the G lanes with shuffles.  The gate/up kernel packs its
+// tile of h = silu(g) * u into digit planes for the down kernel.
 #include "mer_internal.hpp"
 
 namespace mer {
@@ -32,19 +35,6 @@ __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll
   for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
-}
-
-// Resolve the expert blob of instance `inst`.
-__device__ __forceinline__ const uint8_t *resolve_expert(const ProjParams &p, uint32_t inst) {
-  if (p.single) return p.single;
-  const int32_t id = p.ids[inst];
-  if (id < 0 || (uint32_t)id >= p.table_len) {
-    record_status(16u /* MER_ERR_RESIDENCY_MISS */);
-    return nullptr;
-  }
-  const uint8_t *b = reinterpret_cast<const uint8_t *>(p.table[id]);
-  if (!b) record_status(16u);
-  return b;
 }
 
 // Quantise `nblocks` 32-element blocks of the f32 vector `x` into digit
@@ -98,61 +88,67 @@ __device__ __forceinline__ void pack_vector(const float *x, uint32_t nblocks, ui
   }
 }
 
+// One workgroup per token: pack x[t] (fast path only) and resolve the blob
+// pointer of each of the token's expert slots.  An id outside the table or
+// a non-resident entry resolves to null and records a residency miss.
+template <int FMT>
+__global__ __launch_bounds__(256) void prep_kernel(PrepParams q) {
+  const uint32_t t = blockIdx.x;
+  if (threadIdx.x < q.top_k) {
+    const uint32_t inst = t * q.top_k + threadIdx.x;
+    const uint8_t *ptr = q.single;
+    if (!ptr) {
+      const int32_t id = q.ids[inst];
+      if (id < 0 || (uint32_t)id >= q.table_len) {
+        record_status(16u /* MER_ERR_RESIDENCY_MISS */);
+      } else {
+        ptr = reinterpret_cast<const uint8_t *>(q.table[id]);
+        if (!ptr) record_status(16u);
+      }
+    }
+    q.inst_ptr[inst] = ptr;
+  }
+  if (q.xq_dig) {
+    const size_t b0 = (size_t)t * q.blocks;
+    pack_vector<FMT>(q.x + (size_t)t * q.d_model, q.blocks, q.xq_dig + b0 * kBlockDigitDwords, q.xq_scale + b0);
+  }
+}
+
 template <int FMT, int G, int CPL, int R, bool FUSED>
 __global__ __launch_bounds__(256) void proj_kernel(ProjParams p) {
   using T = FmtTraits<FMT>;
   constexpr int kGroups = 64 / G;
   constexpr int kStreams = FUSED ? 2 : 1;
-  extern __shared__ uint32_t smem[];
-  uint32_t *s_dig = smem;
-  float *s_scale = reinterpret_cast<float *>(smem + (size_t)p.lds_blocks * kBlockDigitDwords);
-  float *s_h = s_scale + p.lds_blocks;
+  constexpr uint32_t kStep = R * kGroups;  // rows a wave advances per pass
+  static_assert(kRowsPerWave % kStep == 0, "passes must tile the wave's rows");
+  __shared__ float s_h[kTileRows];
 
-  const uint32_t per_inst = p.slices * p.wgs_per_slice;
+  const uint32_t per_inst = p.slices * p.tiles;
   const uint32_t inst = blockIdx.x / per_inst;
   const uint32_t rem = blockIdx.x % per_inst;
-  const uint32_t slice = rem / p.wgs_per_slice;
-  const uint32_t wgi = rem % p.wgs_per_slice;
+  const uint32_t slice = rem / p.tiles;
+  const uint32_t tile = rem % p.tiles;
   const uint32_t wave = threadIdx.x / 64u;
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t grp = lane / G;
   const uint32_t gl = lane % G;
-  const uint32_t rows_per_wg = 4u * p.rows_per_wave;
-  const uint32_t wg_r0 = wgi * rows_per_wg;
-  const uint32_t wg_rows = min(rows_per_wg, p.rows - wg_r0);
-  const uint32_t r_begin = wg_r0 + wave * p.rows_per_wave;
-  const uint32_t r_end = min(p.rows, r_begin + p.rows_per_wave);
+  const uint32_t tile_r0 = tile * kTileRows;
+  const uint32_t r_end = min(p.rows, tile_r0 + (wave + 1) * kRowsPerWave);
   const uint32_t c_begin = slice * p.chunks_per_slice;
   const uint32_t c_count = min(p.chunks_per_slice, p.chunks - c_begin);
 
-  const uint8_t *expert = resolve_expert(p, inst);
-  if (!expert) {  // uniform over the workgroup: zero this workgroup's outputs
+  const uint8_t *expert = p.inst_ptr[inst];
+  if (!expert) {  // uniform over the workgroup: this tile contributes zeros
     if constexpr (FUSED) {
-      const size_t b0 = (size_t)inst * p.hq_blocks + wg_r0 / 32;
-      for (uint32_t i = threadIdx.x; i < wg_rows / 32 * kBlockDigitDwords; i += blockDim.x)
-        p.hq_dig[b0 * kBlockDigitDwords + i] = 0u;
-      for (uint32_t i = threadIdx.x; i < wg_rows / 32; i += blockDim.x) p.hq_scale[b0 + i] = 0.f;
+      const size_t b0 = (size_t)inst * p.hq_blocks + tile_r0 / 32;
+      if (threadIdx.x < kBlockDigitDwords) p.hq_dig[b0 * kBlockDigitDwords + threadIdx.x] = 0u;
+      if (threadIdx.x == 0) p.hq_scale[b0] = 0.f;
     } else {
       float *out = p.out + ((size_t)inst * p.slices + slice) * p.rows;
-      for (uint32_t r = wg_r0 + threadIdx.x; r < wg_r0 + wg_rows; r += blockDim.x) out[r] = 0.f;
+      if (threadIdx.x < kTileRows) out[tile_r0 + threadIdx.x] = 0.f;
     }
     return;
   }
-
-  // 1. this slice of the input vector -> LDS digit planes
-  if constexpr (FUSED) {
-    const float *x = p.x + (size_t)(inst / p.x_div) * p.x_stride + (size_t)c_begin * 64;
-    pack_vector<FMT>(x, 2 * c_count, s_dig, s_scale);
-  } else {
-    const size_t b0 = (size_t)inst * p.xq_blocks + 2 * (size_t)c_begin;
-    const uint4 *src = reinterpret_cast<const uint4 *>(p.xq_dig + b0 * kBlockDigitDwords);
-    uint4 *dst = reinterpret_cast<uint4 *>(s_dig);
-    const uint32_t n16 = 2 * c_count * kBlockDigitDwords / 4;
-    for (uint32_t i = threadIdx.x; i < n16; i += blockDim.x) dst[i] = src[i];
-    for (uint32_t i = threadIdx.x; i < 2 * c_count; i += blockDim.x) s_scale[i] = p.xq_scale[b0 + i];
-  }
-  __syncthreads();
-
   const uint8_t *w0 = expert + p.proj_off0;
   const uint8_t *w1 = expert + p.proj_off1;  // up projection (FUSED only)
   const size_t row_bytes = (size_t)p.chunks * T::kChunkBytes;
@@ -165,29 +161,8 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjParams p) {
     valid[i] = lchunk[i] < c_count;
   }
 
-  // input digits of the lane's chunk (register-resident when CPL == 1)
-  uint32_t xd[2 * kBlockDigitDwords];
-  float xsc[2];
-  auto fetch_x = [&](int i) {
-    if (valid[i]) {
-      const uint4 *d4 = reinterpret_cast<const uint4 *>(s_dig + (size_t)lchunk[i] * 2 * kBlockDigitDwords);
-#pragma unroll
-      for (int k = 0; k < 2 * kBlockDigitDwords / 4; ++k) {
-        const uint4 v = d4[k];
-        xd[4 * k] = v.x; xd[4 * k + 1] = v.y; xd[4 * k + 2] = v.z; xd[4 * k + 3] = v.w;
-      }
-      xsc[0] = s_scale[2 * lchunk[i]];
-      xsc[1] = s_scale[2 * lchunk[i] + 1];
-    } else {
-#pragma unroll
-      for (int k = 0; k < 2 * kBlockDigitDwords; ++k) xd[k] = 0u;
-      xsc[0] = xsc[1] = 0.f;
-    }
-  };
-  if constexpr (CPL == 1) fetch_x(0);
-
-  for (uint32_t r0 = r_begin + grp * R; r0 < r_end; r0 += R * kGroups) {
-    uint32_t wbuf[kStreams][CPL][R][T::kChunkDwords];
+  using WBuf = uint32_t[kStreams][CPL][R][T::kChunkDwords];
+  auto load_pass = [&](uint32_t r0, WBuf &wb) {
 #pragma unroll
     for (int sidx = 0; sidx < kStreams; ++sidx)
 #pragma unroll
@@ -197,12 +172,38 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjParams p) {
           if (valid[i] && r0 + j < r_end) {
             const uint8_t *base = (sidx == 0 ? w0 : w1) + (size_t)(r0 + j) * row_bytes +
                                   (size_t)(c_begin + lchunk[i]) * T::kChunkBytes;
-            load_chunk<FMT>(base, wbuf[sidx][i][j]);
+            load_chunk<FMT>(base, wb[sidx][i][j]);
           } else {
 #pragma unroll
-            for (int k = 0; k < T::kChunkDwords; ++k) wbuf[sidx][i][j][k] = 0u;
+            for (int k = 0; k < T::kChunkDwords; ++k) wb[sidx][i][j][k] = 0u;
           }
         }
+  };
+
+  // input digits of the lane's chunk (its slice of x or h), from global
+  const size_t xb0 = (size_t)(inst / p.x_div) * p.xq_blocks + 2 * (size_t)c_begin;
+  uint32_t xd[2 * kBlockDigitDwords];
+  float xsc[2];
+  auto fetch_x = [&](int i) {
+    if (valid[i]) {
+      const size_t b = xb0 + 2 * (size_t)lchunk[i];
+      const uint4 *d4 = reinterpret_cast<const uint4 *>(p.xq_dig + b * kBlockDigitDwords);
+#pragma unroll
+      for (int k = 0; k < 2 * kBlockDigitDwords / 4; ++k) {
+        const uint4 v = d4[k];
+        xd[4 * k] = v.x; xd[4 * k + 1] = v.y; xd[4 * k + 2] = v.z; xd[4 * k + 3] = v.w;
+      }
+      const float2 sc = *reinterpret_cast<const float2 *>(p.xq_scale + b);
+      xsc[0] = sc.x;
+      xsc[1] = sc.y;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 2 * kBlockDigitDwords; ++k) xd[k] = 0u;
+      xsc[0] = xsc[1] = 0.f;
+    }
+  };
+
+  auto compute_pass = [&](uint32_t r0, WBuf &wb) {
     float acc[kStreams][R];
 #pragma unroll
     for (int sidx = 0; sidx < kStreams; ++sidx)
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjParams p) {
 #pragma unroll
       for (int sidx = 0; sidx < kStreams; ++sidx)
 #pragma unroll
-        for (int j = 0; j < R; ++j) acc[sidx][j] += chunk_idot<FMT>(wbuf[sidx][i][j], xd, xsc);
+        for (int j = 0; j < R; ++j) acc[sidx][j] += chunk_idot<FMT>(wb[sidx][i][j], xd, xsc);
     }
 #pragma unroll
     for (int sidx = 0; sidx < kStreams; ++sidx)
@@ -227,7 +228,7 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjParams p) {
         if (r < r_end) {
           if constexpr (FUSED) {
             const float h = silu_mul(acc[0][j], acc[1][j]);
-            s_h[r - wg_r0] = h;
+            s_h[r - tile_r0] = h;
             if (p.out) p.out[(size_t)inst * p.rows + r] = h;
           } else {
             p.out[((size_t)inst * p.slices + slice) * p.rows + r] = acc[0][j];
@@ -235,13 +236,33 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjParams p) {
         }
       }
     }
+  };
+
+  // Software-pipelined walk over the wave's rows: pass n+1's loads are
+  // issued before pass n is computed (two register buffers, unrolled by 2).
+  uint32_t r0 = tile_r0 + wave * kRowsPerWave + grp * R;
+  if (r0 < r_end) {
+    WBuf wa, wb;
+    load_pass(r0, wa);
+    if constexpr (CPL == 1) fetch_x(0);
+    while (true) {
+      const uint32_t r1 = r0 + kStep;
+      if (r1 < r_end) load_pass(r1, wb);
+      compute_pass(r0, wa);
+      if (r1 >= r_end) break;
+      const uint32_t r2 = r1 + kStep;
+      if (r2 < r_end) load_pass(r2, wa);
+      compute_pass(r1, wb);
+      if (r2 >= r_end) break;
+      r0 = r2;
+    }
   }
 
   if constexpr (FUSED) {
-    // 3. this workgroup's h rows -> digit planes for the down projection
+    // this tile of h -> digit planes for the down projection
     __syncthreads();
-    const size_t b0 = (size_t)inst * p.hq_blocks + wg_r0 / 32;
-    pack_vector<FMT>(s_h, wg_rows / 32, p.hq_dig + b0 * kBlockDigitDwords, p.hq_scale + b0);
+    const size_t b0 = (size_t)inst * p.hq_blocks + tile_r0 / 32;
+    pack_vector<FMT>(s_h, kTileRows / 32, p.hq_dig + b0 * kBlockDigitDwords, p.hq_scale + b0);
   }
 }
 
@@ -249,13 +270,13 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjParams p) {
 // row, weights decoded element by element in the reference's flat block
 // order (q8_0_matvec_scalar_flat, inference.rs:3618-3632).
 template <int FMT>
-__global__ __launch_bounds__(256) void generic_kernel(ProjParams p, uint32_t cols, int fused) {
+__global__ __launch_bounds__(256) void generic_kernel(GenericParams p) {
   const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
   const uint32_t inst = t / p.rows;
   if (inst >= p.n_inst) return;
   const uint32_t r = t % p.rows;
   float *out = p.out + (size_t)inst * p.rows;
-  const uint8_t *expert = resolve_expert(p, inst);
+  const uint8_t *expert = p.inst_ptr[inst];
   if (!expert) {
     out[r] = 0.f;
     return;
@@ -264,13 +285,13 @@ __global__ __launch_bounds__(256) void generic_kernel(ProjParams p, uint32_t col
   const uint8_t *g = expert + p.proj_off0;
   const uint8_t *u = expert + p.proj_off1;
   float ag = 0.f, au = 0.f;
-  for (uint32_t c = 0; c < cols; ++c) {
-    const size_t flat = (size_t)r * cols + c;
+  for (uint32_t c = 0; c < p.cols; ++c) {
+    const size_t flat = (size_t)r * p.cols + c;
     const float xv = x[c];
     ag = __builtin_fmaf(flat_weight<FMT>(g, flat), xv, ag);
-    if (fused) au = __builtin_fmaf(flat_weight<FMT>(u, flat), xv, au);
+    if (p.fused) au = __builtin_fmaf(flat_weight<FMT>(u, flat), xv, au);
   }
-  out[r] = fused ? silu_mul(ag, au) : ag;
+  out[r] = p.fused ? silu_mul(ag, au) : ag;
 }
 
 // out[t][j] = base + sum_i w[t,i] * sum_s partial[t,i,s][j]
@@ -385,42 +406,45 @@ __global__ __launch_bounds__(256) void fill_kernel(uint64_t seed, uint64_t exper
 
 template <int FMT, int G, int CPL, int R, bool FUSED>
 static hipError_t launch_proj_t(const ProjParams &p, hipStream_t st) {
-  const uint32_t blocks = p.n_inst * p.slices * p.wgs_per_slice;
-  const size_t lds = proj_lds_bytes(p, FUSED);
-  hipLaunchKernelGGL((proj_kernel<FMT, G, CPL, R, FUSED>), dim3(blocks), dim3(256), lds, st, p);
+  const uint32_t blocks = p.n_inst * p.slices * p.tiles;
+  hipLaunchKernelGGL((proj_kernel<FMT, G, CPL, R, FUSED>), dim3(blocks), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
-template <int FMT, bool FUSED, int R>
+// R: rows per pass and lane group; G * ... must tile the 8 rows of a wave.
+template <int FMT, bool FUSED>
 static hipError_t launch_proj_fmt(const ProjParams &p, int G, int CPL, hipStream_t st) {
-  if (G == 16) return launch_proj_t<FMT, 16, 1, R, FUSED>(p, st);
-  if (G == 32) return launch_proj_t<FMT, 32, 1, R, FUSED>(p, st);
+  if (G == 16) return launch_proj_t<FMT, 16, 1, 2, FUSED>(p, st);
+  if (G == 32) return launch_proj_t<FMT, 32, 1, FUSED ? 2 : 4, FUSED>(p, st);
   switch (CPL) {
-    case 1: return launch_proj_t<FMT, 64, 1, R, FUSED>(p, st);
-    case 2: return launch_proj_t<FMT, 64, 2, R, FUSED>(p, st);
-    case 3: return launch_proj_t<FMT, 64, 3, R, FUSED>(p, st);
-    case 4: return launch_proj_t<FMT, 64, 4, R, FUSED>(p, st);
+    case 1: return launch_proj_t<FMT, 64, 1, FUSED ? 2 : 4, FUSED>(p, st);
+    case 2: return launch_proj_t<FMT, 64, 2, 1, FUSED>(p, st);
+    case 3: return launch_proj_t<FMT, 64, 3, 1, FUSED>(p, st);
+    case 4: return launch_proj_t<FMT, 64, 4, 1, FUSED>(p, st);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t launch_proj(int fmt, bool fused, const ProjPlan &plan, const ProjParams &p, hipStream_t st) {
-  if (fmt == FMT_Q4_0) {
-    return fused ? launch_proj_fmt<FMT_Q4_0, true, kFusedRows>(p, plan.G, plan.CPL, st)
-                 : launch_proj_fmt<FMT_Q4_0, false, kDownRows>(p, plan.G, plan.CPL, st);
-  }
-  return fused ? launch_proj_fmt<FMT_Q8_0, true, kFusedRows>(p, plan.G, plan.CPL, st)
-               : launch_proj_fmt<FMT_Q8_0, false, kDownRows>(p, plan.G, plan.CPL, st);
+  if (fmt == FMT_Q4_0)
+    return fused ? launch_proj_fmt<FMT_Q4_0, true>(p, plan.G, plan.CPL, st)
+                 : launch_proj_fmt<FMT_Q4_0, false>(p, plan.G, plan.CPL, st);
+  return fused ? launch_proj_fmt<FMT_Q8_0, true>(p, plan.G, plan.CPL, st)
+               : launch_proj_fmt<FMT_Q8_0, false>(p, plan.G, plan.CPL, st);
 }
 
-hipError_t launch_generic(int fmt, bool fused, const ProjParams &p, uint32_t cols, hipStream_t st) {
+hipError_t launch_prep(int fmt, const PrepParams &q, uint32_t n_tokens, hipStream_t st) {
+  if (fmt == FMT_Q4_0) hipLaunchKernelGGL(prep_kernel<FMT_Q4_0>, dim3(n_tokens), dim3(256), 0, st, q);
+  else hipLaunchKernelGGL(prep_kernel<FMT_Q8_0>, dim3(n_tokens), dim3(256), 0, st, q);
+  return hipGetLastError();
+}
+
+hipError_t launch_generic(int fmt, const GenericParams &p, hipStream_t st) {
   const uint64_t threads = (uint64_t)p.n_inst * p.rows;
   const uint32_t blocks = (uint32_t)((threads + 255) / 256);
   if (blocks == 0) return hipSuccess;
-  if (fmt == FMT_Q4_0)
-    hipLaunchKernelGGL(generic_kernel<FMT_Q4_0>, dim3(blocks), dim3(256), 0, st, p, cols, fused ? 1 : 0);
-  else
-    hipLaunchKernelGGL(generic_kernel<FMT_Q8_0>, dim3(blocks), dim3(256), 0, st, p, cols, fused ? 1 : 0);
+  if (fmt == FMT_Q4_0) hipLaunchKernelGGL(generic_kernel<FMT_Q4_0>, dim3(blocks), dim3(256), 0, st, p);
+  else hipLaunchKernelGGL(generic_kernel<FMT_Q8_0>, dim3(blocks), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -468,6 +492,12 @@ hipError_t launch_fill(int fmt, uint64_t seed, uint64_t expert, uint64_t block_b
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+uint32_t *device_status_ptr() {
+  void *ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_device_status)) != hipSuccess) return nullptr;
+  return reinterpret_cast<uint32_t *>(ptr);
 }
 
 hipError_t read_and_clear_device_status(uint32_t *out) {

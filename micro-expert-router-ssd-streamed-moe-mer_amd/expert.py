@@ -33,6 +33,7 @@ EXPERT_SIZE_TOLERANCE_BYTES = 4096  # inference.rs:3962
 
 MOE_RESIDUAL = 1
 MOE_ACCUMULATE = 2
+MOE_CHAIN = 4
 
 
 def _device_index(t: torch.Tensor) -> int:
@@ -176,6 +177,36 @@ def moe_forward(dtype: WeightDtype, d_model: int, d_ff: int, table: torch.Tensor
     return out
 
 
+def moe_forward_layers(dtype: WeightDtype, d_model: int, d_ff: int, layers, *, residual: bool = False,
+                       accumulate: bool = False, chain: bool = False) -> None:
+    """All MoE layers of one decode step in a single persistent launch: the
+    per-layer WeightedInto step of moe_step_inner (engine.rs:5548-5639) for
+    every layer (model.rs:2715-2741), layers in order.
+
+    `layers` is a sequence of dicts with device tensors: table (int64 [E]),
+    ids (int32 [n_tokens, top_k]), weights (f32 [n_tokens, top_k]),
+    x (f32 [n_tokens, d_model]; may be None for layers > 0 with chain=True)
+    and out (f32 [n_tokens, d_model]).
+    """
+    if not layers:
+        return
+    first = layers[0]
+    _init_for(first["out"])
+    n_tokens, top_k = first["ids"].shape
+    arr = (_lib.MerLayerArgs * len(layers))()
+    for i, la in enumerate(layers):
+        if la["ids"].shape != (n_tokens, top_k) or la["weights"].shape != (n_tokens, top_k):
+            raise ValueError("every layer needs the same [n_tokens, top_k] routing shape")
+        if la["out"].shape != (n_tokens, d_model):
+            raise ValueError("out must be [n_tokens, d_model]")
+        x = la.get("x")
+        arr[i] = _lib.MerLayerArgs(_ptr(la["table"], torch.int64), la["table"].numel(), _ptr(la["ids"], torch.int32),
+                                   _ptr(la["weights"], torch.float32), 0 if x is None else _ptr(x, torch.float32),
+                                   _ptr(la["out"], torch.float32))
+    flags = (MOE_RESIDUAL if residual else 0) | (MOE_ACCUMULATE if accumulate else 0) | (MOE_CHAIN if chain else 0)
+    _call("mer_hip_moe_forward_layers", int(dtype), d_model, d_ff, len(layers), n_tokens, top_k, arr, flags, _stream())
+
+
 def fill_synthetic(dtype: WeightDtype, seed: int, expert_index: int, n_blocks: int, scale_lo: float,
                    scale_hi: float, out: torch.Tensor, block_begin: int = 0) -> torch.Tensor:
     """This library's counter-based synthetic GGUF block generator."""
@@ -194,7 +225,7 @@ def take_device_status() -> None:
     _call("mer_hip_take_device_status")
 
 
-STAGES = ("gate_up", "down", "combine")
+STAGES = ("gate_up", "down", "combine", "prep", "decode")
 
 
 def stage_timing_enable(enable: bool = True) -> None:
@@ -206,7 +237,7 @@ def stage_timing_enable(enable: bool = True) -> None:
 def stage_timing_read() -> dict[str, tuple[float, int]]:
     """{stage: (total_ms, launches)} since the last enable/read (syncs)."""
     init()
-    ms = (ctypes.c_double * 3)()
-    counts = (ctypes.c_uint64 * 3)()
+    ms = (ctypes.c_double * len(STAGES))()
+    counts = (ctypes.c_uint64 * len(STAGES))()
     _call("mer_hip_stage_timing_read", ms, counts)
     return {name: (ms[i], int(counts[i])) for i, name in enumerate(STAGES)}
