@@ -82,6 +82,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0xC0FFEE)
+    ap.add_argument("--per-layer", action="store_true",
+                    help="one mer_hip_moe_forward call per layer instead of one multi-layer launch per token")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -135,11 +137,29 @@ def main() -> int:
         return [(4, dm, dff, 1, K, table[l].data_ptr(), E, ids_d[s, l].data_ptr(), wts_d[s, l].data_ptr(),
                  xs_d[l].data_ptr(), out.data_ptr(), 2, stream) for l in range(L)]
 
-    all_args = [step_args(s) for s in range(total_steps)]
+    # one multi-layer launch per token: prebuilt mer_layer_args arrays
+    fn_layers = lib.mer_hip_moe_forward_layers
+
+    def layer_array(s):
+        arr = (mer._lib.MerLayerArgs * L)()
+        for l in range(L):
+            arr[l] = mer._lib.MerLayerArgs(table[l].data_ptr(), E, ids_d[s, l].data_ptr(), wts_d[s, l].data_ptr(),
+                                           xs_d[l].data_ptr(), out.data_ptr())
+        return arr
+
+    if args.per_layer:
+        all_args = [step_args(s) for s in range(total_steps)]
+    else:
+        all_args = [(4, dm, dff, L, 1, K, layer_array(s), 2, stream) for s in range(total_steps)]
 
     def run_step(s):
-        for a in all_args[s]:
-            rc = fn(*a)
+        if args.per_layer:
+            for a in all_args[s]:
+                rc = fn(*a)
+                if rc:
+                    mer.errors.raise_for_status(rc)
+        else:
+            rc = fn_layers(*all_args[s])
             if rc:
                 mer.errors.raise_for_status(rc)
 
@@ -173,7 +193,9 @@ def main() -> int:
     per_layer_bytes = K * ebytes + 3 * dm * 4  # + x_l in, out read + written
     token_bytes = L * per_layer_bytes
     prep_bytes = dm * 4 + dm // 32 * 100 + K * 12                 # x in, digit planes out, slot pointers
-    stage_bytes = {"gate_up": gate_up_bytes, "down": down_bytes, "combine": combine_bytes, "prep": prep_bytes}
+    decode_bytes = per_layer_bytes if args.per_layer else token_bytes   # one decode_kernel launch
+    stage_bytes = {"gate_up": gate_up_bytes, "down": down_bytes, "combine": combine_bytes, "prep": prep_bytes,
+                   "decode": decode_bytes}
     stage_info = {}
     for name, (ms, cnt) in stages.items():
         if cnt:
@@ -207,7 +229,8 @@ def main() -> int:
                    "bytes_per_token": token_bytes, "parallelism": "single-gpu"},
         "hbm_gbps": token_bytes * tokens_per_s / 1e9,
         "hbm_frac_of_peak": token_bytes * tokens_per_s / 1e9 / HBM_PEAK_GBPS,
-        "roofline": {"bound": "hbm", "kernel": f"proj_kernel ({dominant})", "achieved": dom["gbps"],
+        "roofline": {"bound": "hbm", "kernel": "decode_kernel" if dominant == "decode" else f"proj_kernel ({dominant})",
+                     "achieved": dom["gbps"],
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": dom["gbps"] / HBM_PEAK_GBPS,
                      "traffic": None, "algorithmic_bytes_per_launch": stage_bytes[dominant],
                      "avg_launch_us": dom["avg_us"]},

@@ -111,6 +111,12 @@ int mer_hip_take_device_status(void);
 int mer_hip_stage_timing_enable(int enable);
 int mer_hip_stage_timing_read(double *ms /*[MER_STAGE_COUNT]*/, uint64_t *counts /*[MER_STAGE_COUNT]*/);
 
+/* Item trace of the persistent decode kernel (tracing aid, no reference
+ * counterpart): while set, every launch writes for item i, at record i of
+ * d_records (4 x uint64: item << 32 | XCC id << 16 | low 16 bits of HW_ID, start, inputs ready,
+ * done, in wall-clock ticks of *clock_khz kHz).  NULL disables. */
+int mer_hip_decode_trace(void *d_records, size_t capacity, uint64_t *clock_khz);
+
 /* ---- host-only sizing and validation (no GPU work) ----------------- */
 /* expert_weight_bytes_for (inference.rs:1089-1146); saturates. */
 size_t mer_expert_weight_bytes(int dtype, size_t d_model, size_t d_ff);

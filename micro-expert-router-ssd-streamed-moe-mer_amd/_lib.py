@@ -72,6 +72,7 @@ SIGNATURES = {
     "mer_hip_take_device_status": (c_int, []),
     "mer_hip_stage_timing_enable": (c_int, [c_int]),
     "mer_hip_stage_timing_read": (c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_u64)]),
+    "mer_hip_decode_trace": (c_int, [c_void, c_size, ctypes.POINTER(c_u64)]),
     "mer_expert_weight_bytes": (c_size, [c_int, c_size, c_size]),
     "mer_validate_expert": (c_int, [c_int, c_size, c_size, c_size, c_size, c_size, c_size]),
     "mer_routed_expert_gpu_compatibility": (c_int, [c_int, c_size, c_size]),

@@ -71,6 +71,9 @@ struct DeviceState {
   size_t counter_words = 0;
   uint32_t *status = nullptr;
   uint64_t clock_khz = 100000;
+  uint64_t *trace = nullptr;     // decode item trace buffer (caller-owned)
+  uint64_t trace_cap = 0;
+  uint32_t decode_epoch = 0;     // launches of the decode kernel so far
   int occupancy[2][3][3] = {};   // resident decode workgroups per CU, by (fmt, GG, GD)
 };
 std::mutex g_mu;
@@ -151,7 +154,7 @@ bool capturing(hipStream_t st) {
 // layout the scratch takes (the kernel re-zeroes what it used on exit).
 int ensure_counters(size_t words, hipStream_t st, uint32_t **out) {
   DeviceState &d = g_dev[g_device];
-  words += 64;  // + exit counter
+  words += 2 * kPollStride;  // + abort flag and exit counter, a line each
   if (d.counter_words < words) {
     if (capturing(st))
       return fail(MER_ERR_PHYSICAL_CAPACITY, "decode counters must grow, which cannot happen under graph capture: "
@@ -291,53 +294,49 @@ int run_decode(int dtype, size_t dm, size_t dff, uint32_t n_layers, uint32_t n_t
   p.items_per_layer = p.off_d + p.n_inst * p.d_slices * p.d_tiles;
   p.total_items = (uint64_t)p.items_per_layer * n_layers;
 
-  // counters per layer: R[n_tok] P[n_tok] G-arrive[n_inst*g_tiles] G-done[n_inst*d_slices]
-  //                     D-arrive[n_tok*d_tiles] C-done[n_tok]
-  p.c_r = 0;
-  p.c_p = p.c_r + n_tok;
-  p.c_ga = p.c_p + n_tok;
-  p.c_gd = p.c_ga + p.n_inst * p.g_tiles;
-  p.c_da = p.c_gd + p.n_inst * p.d_slices;
-  p.c_c = p.c_da + n_tok * p.d_tiles;
-  p.cnt_per_layer = p.c_c + n_tok;
+  // counters per layer.  Polled counters (P[n_tok] G-done[n_inst*d_slices]
+  // C-done[n_tok]) sit kPollStride words apart, one per 256-byte line, so waiting
+  // waves spread their polls over the memory channels; arrive-only counters
+  // (G-arrive[n_inst*g_tiles] D-arrive[n_tok*d_tiles]) are packed after them.
+  p.c_p = 0;
+  p.c_gd = p.c_p + n_tok * kPollStride;
+  p.c_c = p.c_gd + p.n_inst * p.d_slices * kPollStride;
+  p.c_ga = p.c_c + n_tok * kPollStride;
+  p.c_da = p.c_ga + p.n_inst * p.g_tiles;
+  p.cnt_per_layer = (p.c_da + n_tok * p.d_tiles + kPollStride - 1) / kPollStride * kPollStride;
   p.n_counters = p.cnt_per_layer * n_layers;
 
   auto up64 = [](size_t v) { return (v + 63) / 64 * 64; };
   const size_t L = n_layers;
-  const size_t n_ptr = up64(L * p.n_inst * 2);
-  const size_t n_xd = up64(L * n_tok * p.xblocks * kBlockDigitDwords);
-  const size_t n_xs = up64(L * n_tok * p.xblocks);
+  const size_t n_xd = L * n_tok * p.xblocks * kLineDwords;
   const size_t n_gp = p.g_slices > 1 ? up64(L * p.n_inst * p.g_slices * 2 * dff) : 0;
-  const size_t n_hd = up64(L * p.n_inst * p.hblocks * kBlockDigitDwords);
-  const size_t n_hs = up64(L * p.n_inst * p.hblocks);
+  const size_t n_hd = L * p.n_inst * p.hblocks * kLineDwords;
   const size_t n_pa = up64(L * p.n_inst * p.d_slices * dm);
   float *scratch = nullptr;
-  if (dev.scratch_floats < n_ptr + n_xd + n_xs + n_gp + n_hd + n_hs + n_pa && capturing(st))
+  if (dev.scratch_floats < n_xd + n_gp + n_hd + n_pa && capturing(st))
     return fail(MER_ERR_PHYSICAL_CAPACITY,
                 "scratch must grow, which cannot happen under graph capture: run the same call once before capturing");
-  int rc = ensure_scratch(n_ptr + n_xd + n_xs + n_gp + n_hd + n_hs + n_pa, &scratch);
+  int rc = ensure_scratch(n_xd + n_gp + n_hd + n_pa, &scratch);
   if (rc) return rc;
   float *cur = scratch;
-  p.inst_ptr = reinterpret_cast<const uint8_t **>(cur);
-  cur += n_ptr;
   p.xq_dig = reinterpret_cast<uint32_t *>(cur);
   cur += n_xd;
-  p.xq_scale = cur;
-  cur += n_xs;
   p.gpart = cur;
   cur += n_gp;
   p.hq_dig = reinterpret_cast<uint32_t *>(cur);
   cur += n_hd;
-  p.hq_scale = cur;
-  cur += n_hs;
   p.partial = cur;
   uint32_t *counters = nullptr;
   if ((rc = ensure_counters(p.n_counters, st, &counters))) return rc;
   p.counters = counters;
   p.exit_count = counters + dev.counter_words - 1;
-  p.abort_flag = counters + dev.counter_words - 2;
+  p.abort_flag = counters + dev.counter_words - kPollStride;
   p.status = dev.status;
   p.timeout_ticks = dev.clock_khz * 2000;  // 2 s per wait
+  p.trace = dev.trace;
+  p.trace_cap = dev.trace_cap;
+  if (++dev.decode_epoch == 0) ++dev.decode_epoch;  // 0 marks never-written scratch
+  p.epoch = dev.decode_epoch;
 
   const void *fn = decode_kernel_fn(fmt, gg.G, gd.G);
   int &occ = dev.occupancy[fmt][g_index(gg.G)][g_index(gd.G)];
@@ -593,6 +592,15 @@ int mer_hip_stage_timing_enable(int enable) {
   if (rc) return rc;
   g_timing = enable != 0;
   g_timed_used = 0;
+  return MER_OK;
+}
+
+int mer_hip_decode_trace(void *d_records, size_t capacity, uint64_t *clock_khz) {
+  int rc = require_init();
+  if (rc) return rc;
+  g_dev[g_device].trace = reinterpret_cast<uint64_t *>(d_records);
+  g_dev[g_device].trace_cap = d_records ? capacity : 0;
+  if (clock_khz) *clock_khz = g_dev[g_device].clock_khz;
   return MER_OK;
 }
 

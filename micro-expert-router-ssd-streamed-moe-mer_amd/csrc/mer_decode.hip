@@ -4,7 +4,8 @@
 // WeightedInto loop of moe_step_inner, engine.rs:5548-5639, over the expert
 // math of inference.rs:3291-3306 / :3636-3746).  A fixed grid of resident
 // one-wave workgroups walks a global list of work items, layer by layer:
-//   R  resolve the blob pointer of a token's expert slots (ids -> table)
+//   R  check a token's expert slots (ids -> table) and report residency
+//      misses; G and D items look their blob up themselves
 //   P  quantise 16 (Q4_0) / 8 (Q8_0) blocks of a token's layer input into
 //      digit planes
 //   G  gate/up of one (slot, column slice, 32-row tile): streams the tile's
@@ -13,15 +14,26 @@
 //   D  down of one (slot, column slice, 32-row tile) -> partial sums; the
 //      last (slot, slice) to arrive for a (token, tile) combines
 //      out = [x +] sum_i w_i y_i for the tile (combine_outputs_into order)
-// Dependencies are counters in global memory: a producer releases its
-// stores (agent-scope fence) and increments; a consumer polls, then
-// acquires.  Items only wait on items earlier in the list, and the grid
-// never exceeds what is co-resident, so the walk always drains; every poll
-// is bounded by a wall-clock timeout that records a device status instead
-// of hanging.  Waves issue the weight loads of their next item's first two
-// passes before waiting on its inputs, so weight streaming overlaps the
-// dependency chain between phases and layers.  The last wave to exit
-// zeroes the counters for the next launch.
+// Dependencies are counters in global memory.  Partial sums and outputs
+// handed from one wave to another are written and read with device-scope
+// (sc1) accesses, which are coherent across the XCDs for exactly the lines
+// they touch.  Digit planes are written with device-scope stores and read
+// with ordinary cached loads, so each XCD's L2 serves the many waves that
+// read the same vector; every digit line carries the epoch of the launch
+// that wrote it, and a reader that finds an older epoch (a copy cached by
+// an earlier launch) reads the line again with device-scope loads.  A
+// producer drains its stores (s_waitcnt vmcnt(0)) and then increments the
+// counter with a device-scope atomic; a consumer polls the counter before
+// reading.  No cache-wide writeback or invalidate is ever issued.  Items
+// only wait on items earlier in the list, and the grid never exceeds what
+// is co-resident, so the walk always drains; every poll is bounded by a
+// wall-clock timeout that records a device status instead of hanging.
+// Waves issue the weight loads of their next item's first passes before
+// waiting on its inputs, so weight streaming overlaps the dependency chain
+// between phases and layers.  The last wave to exit zeroes the counters for
+// the next launch.
+#include <type_traits>
+
 #include "mer_internal.hpp"
 
 namespace mer {
@@ -34,8 +46,40 @@ __device__ __forceinline__ uint32_t poll(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
-__device__ __forceinline__ void release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+// Device-scope (sc1) loads and stores for data exchanged between waves.
+template <class T>
+__device__ __forceinline__ T ld_dev(const T *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ void st_dev(T *p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 16-byte device-scope load (buffer load with the SC1 cache policy).
+__device__ __forceinline__ uint4 ld_dev_b128(const void *base, uint32_t byte_off) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7fffffff, 0x00020000);
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16 /* SC1 */));
+}
+
+// Blob of expert instance `inst` of layer `la` (the same on every lane), or
+// null for a residency miss.  Read from the caller's routing arrays, which
+// were written before this launch, so ordinary loads see them.
+__device__ __forceinline__ const uint8_t *resolve_expert(const DecodeParams &p, const LayerArgs &la, uint32_t inst) {
+  if (p.single) return p.single;
+  const int32_t id = __builtin_amdgcn_readfirstlane(la.ids[inst]);
+  if (id < 0 || (uint32_t)id >= la.table_len) return nullptr;
+  const uint64_t v = reinterpret_cast<const uint64_t *>(la.table)[id];
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const uint8_t *>(((uint64_t)hi << 32) | lo);
+}
+
+// Wait for this wave's outstanding stores; keeps the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void drain_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
 __device__ __forceinline__ void set_status(const DecodeParams &p, uint32_t code) {
   atomicCAS(p.status, 0u, code);
@@ -47,42 +91,63 @@ __device__ __forceinline__ void set_status(const DecodeParams &p, uint32_t code)
 __device__ bool wait_for(const DecodeParams &p, const uint32_t *ctr, uint32_t target) {
   uint32_t ok = 1;
   if (lane_id() == 0 && poll(ctr) < target) {
+    // Exponential backoff from ~0.05 us to ~0.8 us between polls: hundreds of
+    // waiting waves polling at full rate would flood the memory channel that
+    // holds the counter and slow the waves that stream weights.
     const uint64_t t0 = wall_clock64();
+    uint32_t nap = 1, n = 0;
     while (poll(ctr) < target) {
-      if (poll(p.abort_flag) != 0u) {
-        ok = 0;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-      if (wall_clock64() - t0 > p.timeout_ticks) {
-        set_status(p, 24u /* MER_ERR_RUNTIME_INVARIANT: dependency timeout */);
-        __hip_atomic_store(p.abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ok = 0;
-        break;
+      for (uint32_t i = 0; i < nap; ++i) __builtin_amdgcn_s_sleep(2);
+      if (nap < 16) nap <<= 1;
+      if ((++n & 15u) == 0u) {
+        if (poll(p.abort_flag) != 0u) {
+          ok = 0;
+          break;
+        }
+        if (wall_clock64() - t0 > p.timeout_ticks) {
+          set_status(p, 24u /* MER_ERR_RUNTIME_INVARIANT: dependency timeout */);
+          __hip_atomic_store(p.abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ok = 0;
+          break;
+        }
       }
     }
   }
   ok = __shfl(ok, 0, 64);
-  acquire();
+  compiler_fence();
   return ok != 0;
 }
 
-// Release this wave's stores, then count one arrival.
+// Publish this wave's device-scope stores, then count one arrival.
 __device__ __forceinline__ void signal(uint32_t *ctr) {
-  release();
+  drain_stores();
   if (lane_id() == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  compiler_fence();
 }
 
-// Release, count one arrival, and report whether this was the last of
-// `expected` (then acquire the other arrivals' stores).
+// Publish, count one arrival, and report whether this was the last of
+// `expected` (whose stores are then all visible to device-scope loads).
 __device__ __forceinline__ bool arrive_last(uint32_t *ctr, uint32_t expected) {
-  release();
+  drain_stores();
   uint32_t old = 0;
   if (lane_id() == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   old = __shfl(old, 0, 64);
-  const bool last = old + 1 == expected;
-  if (last) acquire();
-  return last;
+  compiler_fence();
+  return old + 1 == expected;
+}
+
+// Optional per-item trace: {item | XCC | HW_ID, t_start, t_ready, t_done} in
+// wall-clock ticks (records beyond trace_cap are dropped).
+__device__ __forceinline__ void trace_item(const DecodeParams &p, uint64_t gi, uint64_t t0, uint64_t t1) {
+  if (!p.trace || lane_id() != 0 || gi >= p.trace_cap) return;
+  uint64_t *r = p.trace + gi * 4;
+  uint32_t hw = 0, xcc = 0;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  r[0] = (gi << 32) | (hw & 0xffffu) | ((xcc & 0xfu) << 16);
+  r[1] = t0;
+  r[2] = t1;
+  r[3] = wall_clock64();
 }
 
 template <int G>
@@ -92,10 +157,11 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-// Quantise `nblocks` (<= 64 / groups) blocks of x into digit planes; one
-// wave, lane = group.
-template <int FMT>
-__device__ __forceinline__ void pack_blocks(const float *x, uint32_t nblocks, uint32_t *dig, float *scale) {
+// Quantise `nblocks` (<= 64 / groups) blocks of x into digit planes in line
+// format (dword 24 = scale, dword 25 = launch epoch); one wave, lane = group.  DEV: x is read with device-scope loads (it may have
+// been written by another wave of this launch); otherwise x is in LDS.
+template <int FMT, bool DEV>
+__device__ __forceinline__ void pack_blocks(const float *x, uint32_t nblocks, uint32_t *dig, uint32_t epoch) {
   using D = DigitTraits<FMT>;
   const uint32_t g = lane_id();
   const bool valid = g < nblocks * D::kGroups;
@@ -105,14 +171,10 @@ __device__ __forceinline__ void pack_blocks(const float *x, uint32_t nblocks, ui
   int finite = 1;
   if (valid) {
     const float *xb = x + (size_t)b * 32;
-    if constexpr (FMT == FMT_Q4_0) {
-      const float4 lo = *reinterpret_cast<const float4 *>(xb + 4 * m);
-      const float4 hi = *reinterpret_cast<const float4 *>(xb + 16 + 4 * m);
-      v[0] = lo.x; v[1] = hi.x; v[2] = lo.y; v[3] = hi.y;
-      v[4] = lo.z; v[5] = hi.z; v[6] = lo.w; v[7] = hi.w;
-    } else {
-      const float4 a = *reinterpret_cast<const float4 *>(xb + 4 * m);
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+#pragma unroll
+    for (int i = 0; i < D::kGroupElems; ++i) {
+      const float *src = xb + group_elem<FMT>((int)m, i);
+      v[i] = DEV ? ld_dev(src) : *src;
     }
 #pragma unroll
     for (int i = 0; i < D::kGroupElems; ++i) {
@@ -132,40 +194,63 @@ __device__ __forceinline__ void pack_blocks(const float *x, uint32_t nblocks, ui
     const BlockScale bs = make_block_scale(amax, finite != 0);
     uint32_t plane[D::kPlanes];
     pack_group<FMT>(v, bs.inv, plane);
+    uint32_t *line = dig + (size_t)b * kLineDwords;
 #pragma unroll
-    for (int k = 0; k < D::kPlanes; ++k) dig[(size_t)b * kBlockDigitDwords + k * D::kGroups + m] = plane[k];
-    if (m == 0) scale[b] = bs.s;
+    for (int k = 0; k < D::kPlanes; ++k) st_dev(line + k * D::kGroups + m, plane[k]);
+    if (m == 0)  // scale and launch epoch, one 8-byte store
+      st_dev(reinterpret_cast<uint64_t *>(line + kBlockDigitDwords),
+             (uint64_t)__float_as_uint(bs.s) | ((uint64_t)epoch << 32));
   }
 }
 
 // Streaming walk of one 32-row tile: lane groups of G lanes, R rows per
-// pass, S weight streams (2 = gate and up).  `emit(row, acc[S])` receives
-// each row's sums (called on all lanes of the owning group).
-template <int FMT, int G, int R, int S>
+// pass, S weight streams (2 = gate and up).  Weight loads are raw buffer
+// loads: a lane without a chunk gets an offset past the buffer's range and
+// reads zeros, so the load sequence is branch-free and the compiler can
+// keep exactly the next passes' loads outstanding.  `emit(row, acc[S])`
+// receives each row's sums on all lanes of the owning group.
+constexpr uint32_t kNoChunk = 0x80000000u;  // beyond num_records: loads return 0
+
+template <int FMT, int G, int R, int S, int NB>
 struct TileWalk {
   using T = FmtTraits<FMT>;
   static constexpr int kGroups = 64 / G;
   static constexpr uint32_t kStep = R * kGroups;
   static constexpr uint32_t kPasses = kTileRows / kStep;
-  static_assert(kTileRows % kStep == 0 && kPasses % 2 == 0, "passes must tile 32 rows in pairs");
+  static_assert(kTileRows % kStep == 0 && kPasses % NB == 0, "passes must tile 32 rows in whole buffer rounds");
   using WBuf = uint32_t[S][R][T::kChunkDwords];
 
-  const uint8_t *w[S];
-  size_t row_bytes;
+  __amdgpu_buffer_rsrc_t rsrc[S];
+  uint32_t row_bytes;
+  uint32_t voff;    // byte offset of the lane's chunk in row r_base (kNoChunk if none)
   uint32_t r_base;  // first row of this lane group's first pass
-  bool valid;       // lane owns a chunk of the slice
+
+  __device__ __forceinline__ void init(const uint8_t *const (&base)[S], uint32_t row_bytes_, uint32_t chunk,
+                                       bool valid, uint32_t r_base_) {
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+      rsrc[s] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base[s]), 0, 0x7fffffff, 0x00020000);
+    row_bytes = row_bytes_;
+    r_base = r_base_;
+    voff = valid ? r_base_ * row_bytes_ + chunk * (uint32_t)T::kChunkBytes : kNoChunk;
+  }
 
   __device__ __forceinline__ void load(uint32_t pass, WBuf &wb) const {
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
       for (int j = 0; j < R; ++j) {
-        if (valid) {
-          load_chunk<FMT>(w[s] + (size_t)(r_base + pass * kStep + j) * row_bytes, wb[s][j]);
-        } else {
+        const uint32_t off = voff + (pass * kStep + j) * row_bytes;
+        constexpr int kVec = T::kChunkDwords / 4;
 #pragma unroll
-          for (int k = 0; k < T::kChunkDwords; ++k) wb[s][j][k] = 0u;
+        for (int v = 0; v < kVec; ++v) {
+          const uint4 q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc[s], off + 16 * v, 0, 0));
+          wb[s][j][4 * v] = q.x;
+          wb[s][j][4 * v + 1] = q.y;
+          wb[s][j][4 * v + 2] = q.z;
+          wb[s][j][4 * v + 3] = q.w;
         }
+        wb[s][j][4 * kVec] = __builtin_amdgcn_raw_buffer_load_b32(rsrc[s], off + 16 * kVec, 0, 0);
       }
   }
 
@@ -185,25 +270,80 @@ struct TileWalk {
       emit(r_base + pass * kStep + j, a);
     }
   }
+
+  // Issue the loads of passes 0 .. NB-1 into the NB buffers.
+  __device__ __forceinline__ void prefetch(WBuf (&w)[NB]) const {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) load(b, w[b]);
+  }
+
+  // Passes 0 .. NB-1 must already be loaded (prefetch).  Each buffer is
+  // refilled with the pass NB ahead as soon as it has been consumed, so NB-1
+  // passes stay in flight while one is computed.  The scheduling barriers
+  // keep the compiler from hoisting one buffer's dot products above another
+  // buffer's loads, which would make each pass wait for loads issued just
+  // before it.
+  template <class Emit>
+  __device__ __forceinline__ void run(WBuf (&w)[NB], const uint32_t *xd, const float *xsc, Emit &&emit) const {
+#pragma unroll 1
+    for (uint32_t pass = 0; pass + NB < kPasses; pass += NB) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        compute(pass + b, w[b], xd, xsc, emit);
+        __builtin_amdgcn_sched_barrier(0);
+        load(pass + NB + b, w[b]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) compute(kPasses - NB + b, w[b], xd, xsc, emit);
+  }
 };
 
-// Fetch the 48 digit dwords and 2 scales of chunk `c` of a packed vector.
-__device__ __forceinline__ void fetch_digits(const uint32_t *dig, const float *sc, size_t block0, bool valid,
+// Fetch the 48 digit dwords and 2 scales of chunk `c` (blocks block0 and
+// block0 + 1) of a packed vector in line format.  The lines were written in
+// this launch by waves that published a counter this wave has waited on,
+// and were not read in this launch before that.  Ordinary cached loads let
+// each XCD's L2 serve the many waves that read the same vector instead of
+// sending every read to the one memory channel that holds it.  A cache may
+// still hold a copy of a line from an earlier launch (another XCD's
+// device-scope stores do not touch this XCD's L2): such a copy carries an
+// older epoch, and the lane then reads the line again with device-scope
+// loads, which bypass the non-coherent caches.
+__device__ __forceinline__ void fetch_digits(const uint32_t *dig, size_t block0, bool valid, uint32_t epoch,
                                              uint32_t (&xd)[2 * kBlockDigitDwords], float (&xsc)[2]) {
-  if (valid) {
-    const uint4 *d4 = reinterpret_cast<const uint4 *>(dig + block0 * kBlockDigitDwords);
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(dig), 0, 0x7fffffff, 0x00020000);
+  const uint32_t voff = valid ? (uint32_t)(block0 * kLineDwords * 4u) : kNoChunk;
+  uint32_t tag[2];
+  auto fetch = [&](auto aux) {
 #pragma unroll
-    for (int k = 0; k < 2 * kBlockDigitDwords / 4; ++k) {
-      const uint4 v = d4[k];
-      xd[4 * k] = v.x; xd[4 * k + 1] = v.y; xd[4 * k + 2] = v.z; xd[4 * k + 3] = v.w;
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int k = 0; k < kBlockDigitDwords / 4; ++k) {
+        const uint4 v = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 4u * (b * kLineDwords + 4 * k), 0, decltype(aux)::value));
+        xd[b * kBlockDigitDwords + 4 * k] = v.x;
+        xd[b * kBlockDigitDwords + 4 * k + 1] = v.y;
+        xd[b * kBlockDigitDwords + 4 * k + 2] = v.z;
+        xd[b * kBlockDigitDwords + 4 * k + 3] = v.w;
+      }
+      const uint2 st = __builtin_bit_cast(
+          uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff + 4u * (b * kLineDwords + kBlockDigitDwords), 0,
+                                                      decltype(aux)::value));
+      xsc[b] = __uint_as_float(st.x);
+      tag[b] = st.y;
     }
-    const float2 s2 = *reinterpret_cast<const float2 *>(sc + block0);
-    xsc[0] = s2.x;
-    xsc[1] = s2.y;
-  } else {
-#pragma unroll
-    for (int k = 0; k < 2 * kBlockDigitDwords; ++k) xd[k] = 0u;
-    xsc[0] = xsc[1] = 0.f;
+  };
+  fetch(std::integral_constant<int, 0>{});
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt and lgkmcnt unchanged
+  const bool stale = valid && (tag[0] != epoch || tag[1] != epoch);
+  if (__builtin_amdgcn_ballot_w64(stale)) {
+    if (stale) fetch(std::integral_constant<int, 16 /* SC1: device scope */>{});
+    // Waiting here, once, also keeps the compiler's wait-count analysis from
+    // treating the digits as outstanding at the loop header of the walk
+    // (which would drain every weight load on each iteration).
+    __builtin_amdgcn_s_waitcnt(0x0F70);
   }
 }
 
@@ -215,38 +355,31 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
   const uint32_t lane = lane_id();
   using D = DigitTraits<FMT>;
   constexpr uint32_t kPackBlocks = 64 / D::kGroups;
+  // Weight passes kept in registers per wave: four for Q4_0 (144 VGPRs), two
+  // for the twice as large Q8_0 chunks.
+  constexpr int kBuffers = FMT == FMT_Q4_0 ? 4 : 2;
 
   for (uint64_t gi = blockIdx.x; gi < p.total_items; gi += gridDim.x) {
+    const uint64_t t_start = p.trace ? wall_clock64() : 0;
+    uint64_t t_ready = 0;
     const uint32_t l = (uint32_t)(gi / p.items_per_layer);
     const uint32_t j = (uint32_t)(gi % p.items_per_layer);
     const LayerArgs &la = p.layers[l];
     uint32_t *cnt = p.counters + (size_t)l * p.cnt_per_layer;
-    const uint8_t **inst_ptr = p.inst_ptr + (size_t)l * p.n_inst;
-    uint32_t *xq_dig = p.xq_dig + (size_t)l * p.n_tok * p.xblocks * kBlockDigitDwords;
-    float *xq_scale = p.xq_scale + (size_t)l * p.n_tok * p.xblocks;
-    uint32_t *hq_dig = p.hq_dig + (size_t)l * p.n_inst * p.hblocks * kBlockDigitDwords;
-    float *hq_scale = p.hq_scale + (size_t)l * p.n_inst * p.hblocks;
+    uint32_t *xq_dig = p.xq_dig + (size_t)l * p.n_tok * p.xblocks * kLineDwords;
+    uint32_t *hq_dig = p.hq_dig + (size_t)l * p.n_inst * p.hblocks * kLineDwords;
     // layer input of token t
     const float *xsrc = (p.flags & kFlagChain) && l > 0 ? p.layers[l - 1].out : la.x;
 
     if (j < p.off_p) {
-      // ---- R: resolve the token's expert slots ----------------------------
+      // ---- R: report residency misses of the token's expert slots ---------
+      // (G and D items resolve their blob themselves and treat a miss as a
+      // zero expert, so nothing waits on this item.)
       const uint32_t t = j;
-      if (lane < p.top_k) {
-        const uint32_t inst = t * p.top_k + lane;
-        const uint8_t *ptr = p.single;
-        if (!ptr) {
-          const int32_t id = la.ids[inst];
-          if (id < 0 || (uint32_t)id >= la.table_len) {
-            set_status(p, 16u /* MER_ERR_RESIDENCY_MISS */);
-          } else {
-            ptr = reinterpret_cast<const uint8_t *>(la.table[id]);
-            if (!ptr) set_status(p, 16u);
-          }
-        }
-        inst_ptr[inst] = ptr;
+      if (lane < p.top_k && !p.single) {
+        const int32_t id = la.ids[t * p.top_k + lane];
+        if (id < 0 || (uint32_t)id >= la.table_len || !la.table[id]) set_status(p, 16u /* MER_ERR_RESIDENCY_MISS */);
       }
-      signal(cnt + p.c_r + t);
     } else if (j < p.off_g) {
       // ---- P: pack part of the token's layer input ------------------------
       const uint32_t idx = j - p.off_p;
@@ -254,14 +387,14 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       const uint32_t part = idx % p.p_items;
       if (l > 0) {  // layers run in order: layer l reads after layer l-1 wrote
         const uint32_t *prev = p.counters + (size_t)(l - 1) * p.cnt_per_layer + p.c_c;
-        wait_for(p, prev + t, p.d_tiles);
+        wait_for(p, prev + (size_t)t * kPollStride, p.d_tiles);
       }
+      if (p.trace) t_ready = wall_clock64();
       const uint32_t b0 = part * kPackBlocks;
       const uint32_t nb = min(kPackBlocks, p.xblocks - b0);
       const size_t tb = (size_t)t * p.xblocks + b0;
-      pack_blocks<FMT>(xsrc + (size_t)t * p.d_model + (size_t)b0 * 32, nb, xq_dig + tb * kBlockDigitDwords,
-                       xq_scale + tb);
-      signal(cnt + p.c_p + t);
+      pack_blocks<FMT, true>(xsrc + (size_t)t * p.d_model + (size_t)b0 * 32, nb, xq_dig + tb * kLineDwords, p.epoch);
+      signal(cnt + p.c_p + (size_t)t * kPollStride);
     } else if (j < p.off_d) {
       // ---- G: gate/up of one (slot, column slice, tile) -------------------
       const uint32_t idx = j - p.off_g;
@@ -270,26 +403,23 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       const uint32_t tile = (idx % per_inst) / p.g_slices;
       const uint32_t gs = idx % p.g_slices;
       const uint32_t t = inst / p.top_k;
-      wait_for(p, cnt + p.c_r + t, 1);
-      const uint8_t *expert = inst_ptr[inst];
+      const uint8_t *expert = resolve_expert(p, la, inst);
       const uint32_t dslice = tile * 32 / (p.d_cps * 64);
-      using W = TileWalk<FMT, GG, 2, 2>;
+      using W = TileWalk<FMT, GG, 2, 2, kBuffers>;
       const uint32_t grp = lane / GG, gl = lane % GG;
       const uint32_t c_begin = gs * p.g_cps;
       const uint32_t c = c_begin + gl;
+      const bool valid = expert && gl < p.g_cps && c < p.g_chunks;
+      const uint8_t *const bases[2] = {expert, expert + p.proj_bytes};
       W walk;
-      walk.valid = expert && gl < p.g_cps && c < p.g_chunks;
-      walk.row_bytes = (size_t)p.g_chunks * FmtTraits<FMT>::kChunkBytes;
-      walk.w[0] = expert + (size_t)c * FmtTraits<FMT>::kChunkBytes;
-      walk.w[1] = walk.w[0] + p.proj_bytes;
-      walk.r_base = tile * kTileRows + grp * 2;
-      typename W::WBuf wa, wb;
-      walk.load(0, wa);
-      walk.load(1, wb);
-      wait_for(p, cnt + p.c_p + t, p.p_items);
+      walk.init(bases, p.g_chunks * (uint32_t)FmtTraits<FMT>::kChunkBytes, c, valid, tile * kTileRows + grp * 2);
+      typename W::WBuf wbuf[kBuffers];
+      walk.prefetch(wbuf);
+      wait_for(p, cnt + p.c_p + (size_t)t * kPollStride, p.p_items);
+      if (p.trace) t_ready = wall_clock64();
       uint32_t xd[2 * kBlockDigitDwords];
       float xsc[2];
-      fetch_digits(xq_dig, xq_scale, (size_t)t * p.xblocks + 2 * (size_t)c, walk.valid, xd, xsc);
+      fetch_digits(xq_dig, (size_t)t * p.xblocks + 2 * (size_t)c, valid, p.epoch, xd, xsc);
       float *gpart = p.gpart + (((size_t)l * p.n_inst + inst) * p.g_slices + gs) * 2 * p.d_ff;
       const bool single_slice = p.g_slices == 1;
       auto emit = [&](uint32_t r, const float (&a)[2]) {
@@ -297,18 +427,12 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
           if (single_slice) {
             s_h[r - tile * kTileRows] = expert ? silu_mul(a[0], a[1]) : 0.f;
           } else {
-            gpart[r] = a[0];
-            gpart[p.d_ff + r] = a[1];
+            st_dev(gpart + r, a[0]);
+            st_dev(gpart + p.d_ff + r, a[1]);
           }
         }
       };
-#pragma unroll 1
-      for (uint32_t pass = 0; pass < W::kPasses; pass += 2) {
-        walk.compute(pass, wa, xd, xsc, emit);
-        if (pass + 2 < W::kPasses) walk.load(pass + 2, wa);
-        walk.compute(pass + 1, wb, xd, xsc, emit);
-        if (pass + 3 < W::kPasses) walk.load(pass + 3, wb);
-      }
+      walk.run(wbuf, xd, xsc, emit);
       bool pack = single_slice;
       if (!single_slice) {
         pack = arrive_last(cnt + p.c_ga + (size_t)inst * p.g_tiles + tile, p.g_slices);
@@ -317,8 +441,8 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
           const uint32_t r = tile * kTileRows + lane;
           float g = 0.f, u = 0.f;
           for (uint32_t s = 0; s < p.g_slices; ++s) {
-            g += p.gpart[base + (size_t)s * 2 * p.d_ff + r];
-            u += p.gpart[base + (size_t)s * 2 * p.d_ff + p.d_ff + r];
+            g += ld_dev(p.gpart + base + (size_t)s * 2 * p.d_ff + r);
+            u += ld_dev(p.gpart + base + (size_t)s * 2 * p.d_ff + p.d_ff + r);
           }
           s_h[lane] = silu_mul(g, u);
         }
@@ -326,8 +450,8 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       if (pack) {
         __syncthreads();
         const size_t hb = (size_t)inst * p.hblocks + tile;
-        pack_blocks<FMT>(s_h, 1, hq_dig + hb * kBlockDigitDwords, hq_scale + hb);
-        signal(cnt + p.c_gd + (size_t)inst * p.d_slices + dslice);
+        pack_blocks<FMT, false>(s_h, 1, hq_dig + hb * kLineDwords, p.epoch);
+        signal(cnt + p.c_gd + ((size_t)inst * p.d_slices + dslice) * kPollStride);
       }
     } else {
       // ---- D: down of one (slot, column slice, tile) + combine -------------
@@ -339,37 +463,30 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       const uint32_t slot = (rem / p.d_slices) % p.top_k;
       const uint32_t ds = rem % p.d_slices;
       const uint32_t inst = t * p.top_k + slot;
-      wait_for(p, cnt + p.c_r + t, 1);
-      const uint8_t *expert = inst_ptr[inst];
-      using W = TileWalk<FMT, GD, (GD == 16 ? 2 : 4), 1>;
+      const uint8_t *expert = resolve_expert(p, la, inst);
+      using W = TileWalk<FMT, GD, (GD == 16 ? 2 : 4), 1, kBuffers>;
       const uint32_t grp = lane / GD, gl = lane % GD;
       const uint32_t c = ds * p.d_cps + gl;
+      const bool valid = expert && gl < p.d_cps && c < p.d_chunks;
+      const uint8_t *const bases[1] = {expert + 2 * p.proj_bytes};
       W walk;
-      walk.valid = expert && gl < p.d_cps && c < p.d_chunks;
-      walk.row_bytes = (size_t)p.d_chunks * FmtTraits<FMT>::kChunkBytes;
-      walk.w[0] = expert + 2 * p.proj_bytes + (size_t)c * FmtTraits<FMT>::kChunkBytes;
-      walk.r_base = tile * kTileRows + grp * (GD == 16 ? 2 : 4);
-      typename W::WBuf wa, wb;
-      walk.load(0, wa);
-      walk.load(1, wb);
+      walk.init(bases, p.d_chunks * (uint32_t)FmtTraits<FMT>::kChunkBytes, c, valid,
+                tile * kTileRows + grp * (GD == 16 ? 2 : 4));
+      typename W::WBuf wbuf[kBuffers];
+      walk.prefetch(wbuf);
       // the h planes of this column slice
       const uint32_t first_tile = ds * p.d_cps * 2;
       const uint32_t n_tiles = min(p.d_cps * 2, p.g_tiles - first_tile);
-      wait_for(p, cnt + p.c_gd + (size_t)inst * p.d_slices + ds, n_tiles);
+      wait_for(p, cnt + p.c_gd + ((size_t)inst * p.d_slices + ds) * kPollStride, n_tiles);
+      if (p.trace) t_ready = wall_clock64();
       uint32_t xd[2 * kBlockDigitDwords];
       float xsc[2];
-      fetch_digits(hq_dig, hq_scale, (size_t)inst * p.hblocks + 2 * (size_t)c, walk.valid, xd, xsc);
+      fetch_digits(hq_dig, (size_t)inst * p.hblocks + 2 * (size_t)c, valid, p.epoch, xd, xsc);
       float *part = p.partial + (((size_t)l * p.n_inst + inst) * p.d_slices + ds) * p.d_model;
       auto emit = [&](uint32_t r, const float (&a)[1]) {
-        if (gl == 0) part[r] = a[0];
+        if (gl == 0) st_dev(part + r, a[0]);
       };
-#pragma unroll 1
-      for (uint32_t pass = 0; pass < W::kPasses; pass += 2) {
-        walk.compute(pass, wa, xd, xsc, emit);
-        if (pass + 2 < W::kPasses) walk.load(pass + 2, wa);
-        walk.compute(pass + 1, wb, xd, xsc, emit);
-        if (pass + 3 < W::kPasses) walk.load(pass + 3, wb);
-      }
+      walk.run(wbuf, xd, xsc, emit);
       if (arrive_last(cnt + p.c_da + (size_t)t * p.d_tiles + tile, p.top_k * p.d_slices)) {
         // combine_outputs_into order: acc = 0; acc += w_i * y_i by slot;
         // zero-weight slots skipped as in the engine (engine.rs:5575-5580)
@@ -381,33 +498,28 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
             if (la.weights && w == 0.0f) continue;
             const float *pp =
                 p.partial + (((size_t)l * p.n_inst + t * p.top_k + i) * p.d_slices) * p.d_model + r;
-            float y = pp[0];
-            for (uint32_t s = 1; s < p.d_slices; ++s) y += pp[(size_t)s * p.d_model];
+            float y = ld_dev(pp);
+            for (uint32_t s = 1; s < p.d_slices; ++s) y += ld_dev(pp + (size_t)s * p.d_model);
             acc = la.weights ? acc + w * y : acc + y;
           }
           float *o = la.out + (size_t)t * p.d_model + r;
-          if (p.flags & kFlagResidual) *o = xsrc[(size_t)t * p.d_model + r] + acc;
-          else if (p.flags & kFlagAccumulate) *o = *o + acc;
-          else *o = acc;
+          if (p.flags & kFlagResidual) st_dev(o, ld_dev(xsrc + (size_t)t * p.d_model + r) + acc);
+          else if (p.flags & kFlagAccumulate) st_dev(o, ld_dev(o) + acc);
+          else st_dev(o, acc);
         }
-        signal(cnt + p.c_c + t);
+        signal(cnt + p.c_c + (size_t)t * kPollStride);
       }
     }
+    trace_item(p, gi, t_start, t_ready);
   }
 
   // the last wave out zeroes the counters for the next launch
-  release();
-  uint32_t old = 0;
-  if (lane == 0) old = __hip_atomic_fetch_add(p.exit_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  old = __shfl(old, 0, 64);
-  if (old + 1 == gridDim.x) {
-    acquire();
-    for (uint32_t i = lane; i < p.n_counters; i += 64) p.counters[i] = 0u;
+  if (arrive_last(p.exit_count, gridDim.x)) {
+    for (uint32_t i = lane; i < p.n_counters; i += 64) st_dev(p.counters + i, 0u);
     if (lane == 0) {
-      *p.abort_flag = 0u;
-      *p.exit_count = 0u;
+      st_dev(p.abort_flag, 0u);
+      st_dev(p.exit_count, 0u);
     }
-    release();
   }
 }
 

@@ -84,6 +84,8 @@ constexpr uint32_t kFlagResidual = 1u;    // out = x + sum_i w_i y_i
 constexpr uint32_t kFlagAccumulate = 2u;  // out += sum_i w_i y_i
 constexpr uint32_t kFlagChain = 4u;       // layer l > 0 reads layer l-1's out
 constexpr uint32_t kMaxLayers = 64;
+constexpr uint32_t kLineDwords = 32;     // decode digit block: 24 digit dwords, scale, padding
+constexpr uint32_t kPollStride = 64;     // words between polled decode counters (one 256-byte line each)
 
 struct LayerArgs {
   const void *const *table;  // device array of expert blob pointers
@@ -107,20 +109,23 @@ struct DecodeParams {
   uint32_t items_per_layer, off_p, off_g, off_d;
   uint64_t total_items;
   // scratch, all [layer]-major
-  const uint8_t **inst_ptr;  // [L][n_inst]
-  uint32_t *xq_dig;          // [L][n_tok][xblocks][24]
-  float *xq_scale;           // [L][n_tok][xblocks]
+  uint32_t epoch;            // launch number on this device (never 0), tags digit lines
+  // Digit planes in the decode kernel's line format: one 128-byte line per
+  // 32-element block, digit dwords 0..23, the f32 block scale in dword 24 and
+  // the epoch of the launch that wrote it in dword 25.
+  uint32_t *xq_dig;          // [L][n_tok][xblocks][32]
+  uint32_t *hq_dig;          // [L][n_inst][hblocks][32]
   float *gpart;              // [L][n_inst][g_slices][2][d_ff]  (g_slices > 1)
-  uint32_t *hq_dig;          // [L][n_inst][hblocks][24]
-  float *hq_scale;           // [L][n_inst][hblocks]
   float *partial;            // [L][n_inst][d_slices][d_model]
   uint32_t *counters;        // [L][cnt_per_layer], zero between launches
-  uint32_t cnt_per_layer, c_r, c_p, c_ga, c_gd, c_da, c_c;
+  uint32_t cnt_per_layer, c_p, c_ga, c_gd, c_da, c_c;
   uint32_t n_counters;
   uint32_t *exit_count;
   uint32_t *abort_flag;      // set by a timed-out wait; later waits give up
   uint32_t *status;
   uint64_t timeout_ticks;
+  uint64_t *trace;           // optional item trace [trace_cap][4], or null
+  uint64_t trace_cap;
 };
 
 const void *decode_kernel_fn(int fmt, int gg, int gd);
