@@ -41,36 +41,58 @@ def log(msg: str) -> None:
 
 
 def cpu_baseline(mer, blob_dev, x_np, dm, dff, experts_per_token, budget_s, gpu_y):
-    """Oracle (checker) timing on host cores: bounded sample of expert FFNs."""
+    """Oracle (checker) timing on host cores: a bounded sample of expert FFNs.
+
+    Cycles through the sampled experts until `budget_s` of CPU work is
+    timed; each expert's first CPU result is also compared with the GPU's."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import mer_oracle  # noqa: E402  (test infrastructure, used as the checker)
 
     threads = max(1, min(16, os.cpu_count() or 1))
+    hosts = [blob.cpu().numpy() for blob in blob_dev]
     times, max_err = [], 0.0
-    n = 0
-    t_start = time.perf_counter()
-    for blob, gy in zip(blob_dev, gpu_y):
-        host = blob.cpu().numpy()
+    spent = 0.0
+    i = 0
+    while spent < budget_s or i < len(hosts):
+        host = hosts[i % len(hosts)]
         t0 = time.perf_counter()
         y = mer_oracle.q4_0_reference_forward(host, x_np, dm, dff, nthreads=threads)
-        times.append(time.perf_counter() - t0)
-        err = np.abs(y.astype(np.float64) - gy) / (1e-3 + 1e-3 * np.abs(y))
-        max_err = max(max_err, float(err.max()))
-        n += 1
-        if time.perf_counter() - t_start > budget_s:
-            break
+        dt = time.perf_counter() - t0
+        times.append(dt)
+        spent += dt
+        if i < len(hosts):
+            err = np.abs(y.astype(np.float64) - gpu_y[i]) / (1e-3 + 1e-3 * np.abs(y))
+            max_err = max(max_err, float(err.max()))
+        i += 1
     per_expert = float(np.mean(times))
     return {
         "value": 1.0 / (per_expert * experts_per_token),
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{n} Mixtral-shape Q4_0 expert FFNs (dequantise + f32 GEMV, the reference's "
-                   f"q4_0_cpu_reference_forward restated in C, {threads} threads), mean "
-                   f"{per_expert * 1e3:.1f} ms/expert, scaled to {experts_per_token} experts/token"),
+        "sample": (f"{len(times)} Mixtral-shape Q4_0 expert FFNs ({len(hosts)} distinct experts, cycled) with the "
+                   f"reference's q4_0_cpu_reference_forward (dequantise + f32 GEMV) restated in C on {threads} "
+                   f"threads: {spent:.1f} s, mean {per_expert * 1e3:.1f} ms/expert, scaled to "
+                   f"{experts_per_token} experts/token"),
         "ms_per_expert": per_expert * 1e3,
         "parity_worst_ratio": max_err,
     }
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_kernel_mixtral_q4_0_traffic.md")
+
+
+def read_traffic(dominant: str):
+    """HBM bytes per decode launch measured with rocprofv3 FETCH_SIZE and
+    WRITE_SIZE passes (scaled by a copy kernel), as committed under profiles/."""
+    if dominant != "decode" or not os.path.exists(TRAFFIC_FILE):
+        return None
+    import re
+
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", open(TRAFFIC_FILE).read())
+    if not m:
+        return None
+    return {"bytes": int(m.group(1)), "source": os.path.relpath(TRAFFIC_FILE, ROOT)}
 
 
 def main() -> int:
@@ -82,6 +104,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0xC0FFEE)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="after the run, launch a plain elementwise kernel that reads and writes MIB MiB "
+                         "(counter calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--per-layer", action="store_true",
                     help="one mer_hip_moe_forward call per layer instead of one multi-layer launch per token")
     args = ap.parse_args()
@@ -206,7 +231,7 @@ def main() -> int:
     dom = stage_info[dominant]
 
     # Parity of the sampled experts: GPU single-expert forward on x0.
-    sample = [(0, l, int(ids[0, l, 0, i])) for l in range(2) for i in range(K)]
+    sample = [(0, l, int(ids[0, l, 0, i])) for l in range(min(L, 8)) for i in range(K)]
     blobs = [weights[(l * E + e) * ebytes:(l * E + e + 1) * ebytes] for _, l, e in sample]
     xdev = torch.from_numpy(x0[0]).to(dev)
     gpu_y = [mer.q4_0_forward(b, xdev, dm, dff).cpu().numpy().astype(np.float64) for b in blobs]
@@ -236,6 +261,18 @@ def main() -> int:
                      "avg_launch_us": dom["avg_us"]},
         "stages": stage_info,
     }
+    traffic = read_traffic(dominant)
+    if traffic is not None:
+        result["roofline"]["traffic"] = traffic["bytes"]
+        result["roofline"]["traffic_source"] = traffic["source"]
+    if args.copy_calibration > 0:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.add(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 3 launches of add(src, 1) over {args.copy_calibration} MiB in, same out")
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(mer, blobs, x0[0], dm, dff, L * K, args.cpu_seconds, gpu_y)
