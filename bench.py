@@ -107,6 +107,9 @@ def main() -> int:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after the run, launch a plain elementwise kernel that reads and writes MIB MiB "
                          "(counter calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--route-after-prev", action="store_true",
+                    help="layer l's routing is read and its experts streamed only after layer l-1's output is "
+                         "complete (MER_MOE_ROUTE_AFTER_PREV), as when routing is computed from that output")
     ap.add_argument("--per-layer", action="store_true",
                     help="one mer_hip_moe_forward call per layer instead of one multi-layer launch per token")
     args = ap.parse_args()
@@ -175,7 +178,8 @@ def main() -> int:
     if args.per_layer:
         all_args = [step_args(s) for s in range(total_steps)]
     else:
-        all_args = [(4, dm, dff, L, 1, K, layer_array(s), 2, stream) for s in range(total_steps)]
+        flags = 2 | (8 if args.route_after_prev else 0)  # ACCUMULATE [| ROUTE_AFTER_PREV]
+        all_args = [(4, dm, dff, L, 1, K, layer_array(s), flags, stream) for s in range(total_steps)]
 
     def run_step(s):
         if args.per_layer:
@@ -251,7 +255,11 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "mixtral-8x7b-moe-decode-q4_0-top2", "layers": L, "experts_per_layer": E,
                    "top_k": K, "d_model": dm, "d_ff": dff, "batch": 1, "resident_bytes": L * E * ebytes,
-                   "bytes_per_token": token_bytes, "parallelism": "single-gpu"},
+                   "bytes_per_token": token_bytes, "parallelism": "single-gpu",
+                   "launch": "per-layer" if args.per_layer else "all-layers",
+                   "routing": ("each layer's routing used only after the previous layer's output is complete"
+                               if args.per_layer or args.route_after_prev else
+                               "every layer's routing is a launch input (exogenous N(0,1) logits)")},
         "hbm_gbps": token_bytes * tokens_per_s / 1e9,
         "hbm_frac_of_peak": token_bytes * tokens_per_s / 1e9 / HBM_PEAK_GBPS,
         "roofline": {"bound": "hbm", "kernel": "decode_kernel" if dominant == "decode" else f"proj_kernel ({dominant})",

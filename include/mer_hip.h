@@ -194,6 +194,12 @@ typedef struct mer_layer_args {
 } mer_layer_args;
 
 #define MER_MOE_CHAIN 4u /* layer l > 0 reads layer l-1's out as its x */
+/* Layer l > 0 reads its routing (expert_ids, expert_table) and streams its
+ * experts' weights only after layer l-1's output is complete, as a step
+ * whose routing is computed from that output must.  Without this flag the
+ * launch may start streaming layer l's weights while layer l-1 finishes
+ * (the routing of every layer is an input of the launch). */
+#define MER_MOE_ROUTE_AFTER_PREV 8u
 
 /* n_layers (<= 64) routed-expert MoE layers of one decode step in a single
  * persistent launch: the per-layer WeightedInto step of moe_step_inner

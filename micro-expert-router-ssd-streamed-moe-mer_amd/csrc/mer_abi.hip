@@ -766,7 +766,7 @@ int mer_hip_moe_forward_layers(int dtype, size_t d_model, size_t d_ff, size_t n_
     return fail(MER_ERR_UNSUPPORTED_DTYPE, "unsupported expert dtype %d", dtype);
   rc = mer_routed_expert_gpu_compatibility(dtype, d_model, d_ff);
   if (rc) return rc;
-  if (flags & ~(MER_MOE_RESIDUAL | MER_MOE_ACCUMULATE | MER_MOE_CHAIN))
+  if (flags & ~(MER_MOE_RESIDUAL | MER_MOE_ACCUMULATE | MER_MOE_CHAIN | MER_MOE_ROUTE_AFTER_PREV))
     return fail(MER_ERR_INVALID_LAYOUT, "unknown flags 0x%x", flags);
   if ((flags & 3u) == 3u) return fail(MER_ERR_INVALID_LAYOUT, "RESIDUAL and ACCUMULATE are exclusive");
   if (n_layers == 0 || n_tokens == 0 || top_k == 0) return MER_OK;

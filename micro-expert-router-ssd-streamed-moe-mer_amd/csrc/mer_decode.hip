@@ -209,7 +209,8 @@ __device__ __forceinline__ void pack_blocks(const float *x, uint32_t nblocks, ui
 // reads zeros, so the load sequence is branch-free and the compiler can
 // keep exactly the next passes' loads outstanding.  `emit(row, acc[S])`
 // receives each row's sums on all lanes of the owning group.
-constexpr uint32_t kNoChunk = 0x80000000u;  // beyond num_records: loads return 0
+constexpr uint32_t kNoChunk = 0x80000000u;
+constexpr uint32_t kCombineBatch = 16;  // partial sums a combine loads in one batch  // beyond num_records: loads return 0
 
 template <int FMT, int G, int R, int S, int NB>
 struct TileWalk {
@@ -370,12 +371,18 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
     uint32_t *hq_dig = p.hq_dig + (size_t)l * p.n_inst * p.hblocks * kLineDwords;
     // layer input of token t
     const float *xsrc = (p.flags & kFlagChain) && l > 0 ? p.layers[l - 1].out : la.x;
+    // Layer l-1's output for token t is complete (its combine counter).
+    auto wait_prev_layer = [&](uint32_t t) {
+      if (l > 0) wait_for(p, p.counters + (size_t)(l - 1) * p.cnt_per_layer + p.c_c + (size_t)t * kPollStride, p.d_tiles);
+    };
+    const bool route_after_prev = (p.flags & kFlagRouteAfterPrev) != 0;
 
     if (j < p.off_p) {
       // ---- R: report residency misses of the token's expert slots ---------
       // (G and D items resolve their blob themselves and treat a miss as a
       // zero expert, so nothing waits on this item.)
       const uint32_t t = j;
+      if (route_after_prev) wait_prev_layer(t);
       if (lane < p.top_k && !p.single) {
         const int32_t id = la.ids[t * p.top_k + lane];
         if (id < 0 || (uint32_t)id >= la.table_len || !la.table[id]) set_status(p, 16u /* MER_ERR_RESIDENCY_MISS */);
@@ -385,10 +392,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       const uint32_t idx = j - p.off_p;
       const uint32_t t = idx / p.p_items;
       const uint32_t part = idx % p.p_items;
-      if (l > 0) {  // layers run in order: layer l reads after layer l-1 wrote
-        const uint32_t *prev = p.counters + (size_t)(l - 1) * p.cnt_per_layer + p.c_c;
-        wait_for(p, prev + (size_t)t * kPollStride, p.d_tiles);
-      }
+      wait_prev_layer(t);  // layers run in order: layer l reads after layer l-1 wrote
       if (p.trace) t_ready = wall_clock64();
       const uint32_t b0 = part * kPackBlocks;
       const uint32_t nb = min(kPackBlocks, p.xblocks - b0);
@@ -403,6 +407,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       const uint32_t tile = (idx % per_inst) / p.g_slices;
       const uint32_t gs = idx % p.g_slices;
       const uint32_t t = inst / p.top_k;
+      if (route_after_prev) wait_prev_layer(t);
       const uint8_t *expert = resolve_expert(p, la, inst);
       const uint32_t dslice = tile * 32 / (p.d_cps * 64);
       using W = TileWalk<FMT, GG, 2, 2, kBuffers>;
@@ -463,6 +468,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       const uint32_t slot = (rem / p.d_slices) % p.top_k;
       const uint32_t ds = rem % p.d_slices;
       const uint32_t inst = t * p.top_k + slot;
+      if (route_after_prev) wait_prev_layer(t);
       const uint8_t *expert = resolve_expert(p, la, inst);
       using W = TileWalk<FMT, GD, (GD == 16 ? 2 : 4), 1, kBuffers>;
       const uint32_t grp = lane / GD, gl = lane % GD;
@@ -483,31 +489,48 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       float xsc[2];
       fetch_digits(hq_dig, (size_t)inst * p.hblocks + 2 * (size_t)c, valid, p.epoch, xd, xsc);
       float *part = p.partial + (((size_t)l * p.n_inst + inst) * p.d_slices + ds) * p.d_model;
+      // Row sums go to LDS, then out as one 128-byte store.  The slot weight
+      // is applied here; a zero-weight slot contributes exactly nothing, as
+      // the engine skips it (engine.rs:5575-5580).
+      const float w_slot = la.weights ? la.weights[t * p.top_k + slot] : 1.0f;
       auto emit = [&](uint32_t r, const float (&a)[1]) {
-        if (gl == 0) st_dev(part + r, a[0]);
+        if (gl == 0) s_h[r - tile * kTileRows] = a[0];
       };
       walk.run(wbuf, xd, xsc, emit);
+      __syncthreads();
+      if (lane < kTileRows) {
+        const float y = s_h[lane];
+        st_dev(part + tile * kTileRows + lane, (la.weights && w_slot == 0.0f) ? 0.0f : w_slot * y);
+      }
       if (arrive_last(cnt + p.c_da + (size_t)t * p.d_tiles + tile, p.top_k * p.d_slices)) {
-        // combine_outputs_into order: acc = 0; acc += w_i * y_i by slot;
-        // zero-weight slots skipped as in the engine (engine.rs:5575-5580)
+        // out = [x +] sum over slots i (and column slices) of w_i * y_i, in
+        // slot order (combine_outputs_into, inference.rs:4472-4491).  All
+        // device-scope loads are issued before any is used, so the combine
+        // costs one round trip.
         if (lane < kTileRows) {
           const uint32_t r = tile * kTileRows + lane;
-          float acc = 0.f;
-          for (uint32_t i = 0; i < p.top_k; ++i) {
-            const float w = la.weights ? la.weights[t * p.top_k + i] : 1.0f;
-            if (la.weights && w == 0.0f) continue;
-            const float *pp =
-                p.partial + (((size_t)l * p.n_inst + t * p.top_k + i) * p.d_slices) * p.d_model + r;
-            float y = ld_dev(pp);
-            for (uint32_t s = 1; s < p.d_slices; ++s) y += ld_dev(pp + (size_t)s * p.d_model);
-            acc = la.weights ? acc + w * y : acc + y;
-          }
           float *o = la.out + (size_t)t * p.d_model + r;
-          if (p.flags & kFlagResidual) st_dev(o, ld_dev(xsrc + (size_t)t * p.d_model + r) + acc);
-          else if (p.flags & kFlagAccumulate) st_dev(o, ld_dev(o) + acc);
-          else st_dev(o, acc);
+          float base = 0.f;
+          if (p.flags & kFlagResidual) base = ld_dev(xsrc + (size_t)t * p.d_model + r);
+          else if (p.flags & kFlagAccumulate) base = ld_dev(o);
+          const uint32_t n_parts = p.top_k * p.d_slices;
+          const float *pp = p.partial + ((size_t)l * p.n_inst + (size_t)t * p.top_k) * p.d_slices * p.d_model + r;
+          float acc = 0.f;
+          if (n_parts <= kCombineBatch) {
+            float v[kCombineBatch];
+#pragma unroll
+            for (uint32_t k = 0; k < kCombineBatch; ++k) v[k] = k < n_parts ? ld_dev(pp + (size_t)k * p.d_model) : 0.f;
+#pragma unroll
+            for (uint32_t k = 0; k < kCombineBatch; ++k)
+              if (k < n_parts) acc += v[k];
+          } else {
+            for (uint32_t k = 0; k < n_parts; ++k) acc += ld_dev(pp + (size_t)k * p.d_model);
+          }
+          const float val = (p.flags & (kFlagResidual | kFlagAccumulate)) ? base + acc : acc;
+          st_dev(o, val);
         }
         signal(cnt + p.c_c + (size_t)t * kPollStride);
+        compiler_fence();
       }
     }
     trace_item(p, gi, t_start, t_ready);

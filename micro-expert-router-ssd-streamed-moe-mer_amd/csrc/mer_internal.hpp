@@ -83,6 +83,7 @@ struct CombineParams {
 constexpr uint32_t kFlagResidual = 1u;    // out = x + sum_i w_i y_i
 constexpr uint32_t kFlagAccumulate = 2u;  // out += sum_i w_i y_i
 constexpr uint32_t kFlagChain = 4u;       // layer l > 0 reads layer l-1's out
+constexpr uint32_t kFlagRouteAfterPrev = 8u;  // layer l > 0 touches its experts after layer l-1 completes
 constexpr uint32_t kMaxLayers = 64;
 constexpr uint32_t kLineDwords = 32;     // decode digit block: 24 digit dwords, scale, padding
 constexpr uint32_t kPollStride = 64;     // words between polled decode counters (one 256-byte line each)

@@ -34,6 +34,7 @@ EXPERT_SIZE_TOLERANCE_BYTES = 4096  # inference.rs:3962
 MOE_RESIDUAL = 1
 MOE_ACCUMULATE = 2
 MOE_CHAIN = 4
+MOE_ROUTE_AFTER_PREV = 8
 
 
 def _device_index(t: torch.Tensor) -> int:
@@ -178,7 +179,7 @@ def moe_forward(dtype: WeightDtype, d_model: int, d_ff: int, table: torch.Tensor
 
 
 def moe_forward_layers(dtype: WeightDtype, d_model: int, d_ff: int, layers, *, residual: bool = False,
-                       accumulate: bool = False, chain: bool = False) -> None:
+                       accumulate: bool = False, chain: bool = False, route_after_prev: bool = False) -> None:
     """All MoE layers of one decode step in a single persistent launch: the
     per-layer WeightedInto step of moe_step_inner (engine.rs:5548-5639) for
     every layer (model.rs:2715-2741), layers in order.
@@ -186,7 +187,9 @@ def moe_forward_layers(dtype: WeightDtype, d_model: int, d_ff: int, layers, *, r
     `layers` is a sequence of dicts with device tensors: table (int64 [E]),
     ids (int32 [n_tokens, top_k]), weights (f32 [n_tokens, top_k]),
     x (f32 [n_tokens, d_model]; may be None for layers > 0 with chain=True)
-    and out (f32 [n_tokens, d_model]).
+    and out (f32 [n_tokens, d_model]).  route_after_prev: layer l > 0 reads
+    its routing and streams its experts only after layer l-1's output is
+    complete (as when routing is computed from that output).
     """
     if not layers:
         return
@@ -203,7 +206,8 @@ def moe_forward_layers(dtype: WeightDtype, d_model: int, d_ff: int, layers, *, r
         arr[i] = _lib.MerLayerArgs(_ptr(la["table"], torch.int64), la["table"].numel(), _ptr(la["ids"], torch.int32),
                                    _ptr(la["weights"], torch.float32), 0 if x is None else _ptr(x, torch.float32),
                                    _ptr(la["out"], torch.float32))
-    flags = (MOE_RESIDUAL if residual else 0) | (MOE_ACCUMULATE if accumulate else 0) | (MOE_CHAIN if chain else 0)
+    flags = ((MOE_RESIDUAL if residual else 0) | (MOE_ACCUMULATE if accumulate else 0) | (MOE_CHAIN if chain else 0)
+             | (MOE_ROUTE_AFTER_PREV if route_after_prev else 0))
     _call("mer_hip_moe_forward_layers", int(dtype), d_model, d_ff, len(layers), n_tokens, top_k, arr, flags, _stream())
 
 

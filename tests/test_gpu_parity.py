@@ -329,3 +329,69 @@ def test_moe_forward_full_mixtral_top2(mer, oracle, gpu):
     assert_ffn_close(got, w_np[0] * y0 + w_np[1] * y1, "fused vs separate")
     want = oracle.combine_outputs(np.stack([oracle.q4_0_reference_forward(b, x, dm, dff, 16) for b in blobs]), w_np)
     assert_ffn_close(got, want, "fused vs oracle")
+
+
+# ---- all layers of a decode step in one launch ----------------------------
+
+def _oracle_expert(oracle, dtype, blob, x, dm, dff):
+    if dtype == Q4:
+        return oracle.q4_0_reference_forward(blob, x, dm, dff)
+    rc, y = oracle.q8_0_direct_forward(blob, x, dm, dff)
+    assert rc == 0
+    return y
+
+
+def _oracle_moe(oracle, dtype, blobs, ids, w, x, dm, dff):
+    out = np.zeros_like(x)
+    for t in range(x.shape[0]):
+        ys = np.stack([_oracle_expert(oracle, dtype, blobs[ids[t, i]], x[t], dm, dff) for i in range(ids.shape[1])])
+        out[t] = oracle.combine_outputs(ys, w[t])
+    return out
+
+
+LAYER_MODES = [("accumulate", Q4), ("residual", Q4), ("plain", Q4), ("chain", Q4), ("chain_residual", Q4),
+               ("accumulate_strict", Q4), ("chain_residual_strict", Q4), ("accumulate", Q8), ("residual", Q8)]
+
+
+@pytest.mark.parametrize("mode,dtype", LAYER_MODES)
+def test_moe_forward_layers_vs_oracle(mer, oracle, gpu, mode, dtype):
+    """mer_hip_moe_forward_layers against the oracle run layer by layer, for
+    every flag combination; a second launch with new inputs reuses the
+    library's scratch and must not see the first launch's data."""
+    dm, dff, n_layers, n_exp, n_tok, k = 256, 512, 3, 4, 2, 2
+    chain, residual = "chain" in mode, "residual" in mode
+    accumulate, strict = "accumulate" in mode, "strict" in mode
+    say(f"moe layers mode={mode} dtype={dtype}")
+    blobs = [[make_expert(oracle, dtype, dm, dff, l * n_exp + e) for e in range(n_exp)] for l in range(n_layers)]
+    tables = [_table(b, gpu) for b in blobs]
+    rng = np.random.default_rng(31)
+    ids = [np.stack([rng.choice(n_exp, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
+           for _ in range(n_layers)]
+    w = [rng.random((n_tok, k)).astype(np.float32) for _ in range(n_layers)]
+    for launch in range(2):
+        xs = [rng.standard_normal((n_tok, dm)).astype(np.float32) for _ in range(n_layers)]
+        acc0 = rng.standard_normal((n_tok, dm)).astype(np.float32)
+        shared = to_dev(acc0, gpu) if accumulate else None
+        layers = []
+        for l in range(n_layers):
+            layers.append(dict(table=tables[l][1], ids=to_dev(ids[l], gpu), weights=to_dev(w[l], gpu),
+                               x=None if chain and l > 0 else to_dev(xs[l], gpu),
+                               out=shared if accumulate else torch.zeros((n_tok, dm), device=gpu)))
+        mer.moe_forward_layers(mer.WeightDtype(dtype), dm, dff, layers, residual=residual, accumulate=accumulate,
+                               chain=chain, route_after_prev=strict)
+        torch.cuda.synchronize()
+        acc = acc0.copy()
+        prev = None
+        for l in range(n_layers):
+            xin = prev if chain and l > 0 else xs[l]
+            y = _oracle_moe(oracle, dtype, blobs[l], ids[l], w[l], xin, dm, dff)
+            if accumulate:
+                acc = acc + y
+                continue
+            want = xin + y if residual else y
+            assert_ffn_close(layers[l]["out"].cpu().numpy(), want, f"launch {launch} layer {l}")
+            prev = layers[l]["out"].cpu().numpy() if chain else None
+        if accumulate:
+            assert_ffn_close(shared.cpu().numpy(), acc, f"launch {launch} accumulated")
+    mer.take_device_status()
+    del tables
