@@ -136,18 +136,28 @@ __device__ __forceinline__ bool arrive_last(uint32_t *ctr, uint32_t expected) {
   return old + 1 == expected;
 }
 
-// Optional per-item trace: {item | XCC | HW_ID, t_start, t_ready, t_done} in
-// wall-clock ticks (records beyond trace_cap are dropped).
-__device__ __forceinline__ void trace_item(const DecodeParams &p, uint64_t gi, uint64_t t0, uint64_t t1) {
+// Optional per-item trace, 8 x u64 per item: {item << 32 | XCC << 16 | low
+// HW_ID bits, start, inputs ready, digits fetched, walk done, arrived
+// (D items), end, 0} in wall-clock ticks (records beyond trace_cap are
+// dropped; unset marks are 0).
+struct TraceMarks {
+  uint64_t start, ready, fetched, walked, arrived;
+};
+__device__ __forceinline__ uint64_t trace_now(const DecodeParams &p) { return p.trace ? wall_clock64() : 0; }
+__device__ __forceinline__ void trace_item(const DecodeParams &p, uint64_t gi, const TraceMarks &m) {
   if (!p.trace || lane_id() != 0 || gi >= p.trace_cap) return;
-  uint64_t *r = p.trace + gi * 4;
+  uint64_t *r = p.trace + gi * 8;
   uint32_t hw = 0, xcc = 0;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
   r[0] = (gi << 32) | (hw & 0xffffu) | ((xcc & 0xfu) << 16);
-  r[1] = t0;
-  r[2] = t1;
-  r[3] = wall_clock64();
+  r[1] = m.start;
+  r[2] = m.ready;
+  r[3] = m.fetched;
+  r[4] = m.walked;
+  r[5] = m.arrived;
+  r[6] = wall_clock64();
+  r[7] = 0;
 }
 
 template <int G>
@@ -356,13 +366,15 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
   const uint32_t lane = lane_id();
   using D = DigitTraits<FMT>;
   constexpr uint32_t kPackBlocks = 64 / D::kGroups;
-  // Weight passes kept in registers per wave: four for Q4_0 (144 VGPRs), two
-  // for the twice as large Q8_0 chunks.
-  constexpr int kBuffers = FMT == FMT_Q4_0 ? 4 : 2;
+  // Weight passes kept in registers per wave.  Two keep the kernel at 166
+  // VGPRs, three waves per SIMD: a third resident wave per SIMD (the next
+  // layer's items prefetching, a second G or D wave) hides more latency than
+  // two more passes in flight per wave would.
+  constexpr int kBuffers = 2;
 
   for (uint64_t gi = blockIdx.x; gi < p.total_items; gi += gridDim.x) {
-    const uint64_t t_start = p.trace ? wall_clock64() : 0;
-    uint64_t t_ready = 0;
+    TraceMarks tm{};
+    tm.start = trace_now(p);
     const uint32_t l = (uint32_t)(gi / p.items_per_layer);
     const uint32_t j = (uint32_t)(gi % p.items_per_layer);
     const LayerArgs &la = p.layers[l];
@@ -393,7 +405,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       const uint32_t t = idx / p.p_items;
       const uint32_t part = idx % p.p_items;
       wait_prev_layer(t);  // layers run in order: layer l reads after layer l-1 wrote
-      if (p.trace) t_ready = wall_clock64();
+      tm.ready = trace_now(p);
       const uint32_t b0 = part * kPackBlocks;
       const uint32_t nb = min(kPackBlocks, p.xblocks - b0);
       const size_t tb = (size_t)t * p.xblocks + b0;
@@ -421,10 +433,11 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       typename W::WBuf wbuf[kBuffers];
       walk.prefetch(wbuf);
       wait_for(p, cnt + p.c_p + (size_t)t * kPollStride, p.p_items);
-      if (p.trace) t_ready = wall_clock64();
+      tm.ready = trace_now(p);
       uint32_t xd[2 * kBlockDigitDwords];
       float xsc[2];
       fetch_digits(xq_dig, (size_t)t * p.xblocks + 2 * (size_t)c, valid, p.epoch, xd, xsc);
+      tm.fetched = trace_now(p);
       float *gpart = p.gpart + (((size_t)l * p.n_inst + inst) * p.g_slices + gs) * 2 * p.d_ff;
       const bool single_slice = p.g_slices == 1;
       auto emit = [&](uint32_t r, const float (&a)[2]) {
@@ -438,6 +451,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
         }
       };
       walk.run(wbuf, xd, xsc, emit);
+      tm.walked = trace_now(p);
       bool pack = single_slice;
       if (!single_slice) {
         pack = arrive_last(cnt + p.c_ga + (size_t)inst * p.g_tiles + tile, p.g_slices);
@@ -484,10 +498,11 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       const uint32_t first_tile = ds * p.d_cps * 2;
       const uint32_t n_tiles = min(p.d_cps * 2, p.g_tiles - first_tile);
       wait_for(p, cnt + p.c_gd + ((size_t)inst * p.d_slices + ds) * kPollStride, n_tiles);
-      if (p.trace) t_ready = wall_clock64();
+      tm.ready = trace_now(p);
       uint32_t xd[2 * kBlockDigitDwords];
       float xsc[2];
       fetch_digits(hq_dig, (size_t)inst * p.hblocks + 2 * (size_t)c, valid, p.epoch, xd, xsc);
+      tm.fetched = trace_now(p);
       float *part = p.partial + (((size_t)l * p.n_inst + inst) * p.d_slices + ds) * p.d_model;
       // Row sums go to LDS, then out as one 128-byte store.  The slot weight
       // is applied here; a zero-weight slot contributes exactly nothing, as
@@ -497,12 +512,15 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
         if (gl == 0) s_h[r - tile * kTileRows] = a[0];
       };
       walk.run(wbuf, xd, xsc, emit);
+      tm.walked = trace_now(p);
       __syncthreads();
       if (lane < kTileRows) {
         const float y = s_h[lane];
         st_dev(part + tile * kTileRows + lane, (la.weights && w_slot == 0.0f) ? 0.0f : w_slot * y);
       }
-      if (arrive_last(cnt + p.c_da + (size_t)t * p.d_tiles + tile, p.top_k * p.d_slices)) {
+      const bool last = arrive_last(cnt + p.c_da + (size_t)t * p.d_tiles + tile, p.top_k * p.d_slices);
+      tm.arrived = trace_now(p);
+      if (last) {
         // out = [x +] sum over slots i (and column slices) of w_i * y_i, in
         // slot order (combine_outputs_into, inference.rs:4472-4491).  All
         // device-scope loads are issued before any is used, so the combine
@@ -533,7 +551,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
         compiler_fence();
       }
     }
-    trace_item(p, gi, t_start, t_ready);
+    trace_item(p, gi, tm);
   }
 
   // the last wave out zeroes the counters for the next launch
