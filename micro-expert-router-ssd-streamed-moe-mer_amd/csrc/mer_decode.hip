@@ -388,6 +388,12 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       if (l > 0) wait_for(p, p.counters + (size_t)(l - 1) * p.cnt_per_layer + p.c_c + (size_t)t * kPollStride, p.d_tiles);
     };
     const bool route_after_prev = (p.flags & kFlagRouteAfterPrev) != 0;
+    // Under ROUTE_AFTER_PREV, G and D items touch their experts only once the
+    // layer's input is packed (which implies layer l-1 is complete), so the
+    // input packing does not queue behind every wave's weight prefetch.
+    auto wait_input_packed = [&](uint32_t t) {
+      if (l > 0) wait_for(p, cnt + p.c_p + (size_t)t * kPollStride, p.p_items);
+    };
 
     if (j < p.off_p) {
       // ---- R: report residency misses of the token's expert slots ---------
@@ -419,7 +425,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       const uint32_t tile = (idx % per_inst) / p.g_slices;
       const uint32_t gs = idx % p.g_slices;
       const uint32_t t = inst / p.top_k;
-      if (route_after_prev) wait_prev_layer(t);
+      if (route_after_prev) wait_input_packed(t);
       const uint8_t *expert = resolve_expert(p, la, inst);
       const uint32_t dslice = tile * 32 / (p.d_cps * 64);
       using W = TileWalk<FMT, GG, 2, 2, kBuffers>;
@@ -482,7 +488,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       const uint32_t slot = (rem / p.d_slices) % p.top_k;
       const uint32_t ds = rem % p.d_slices;
       const uint32_t inst = t * p.top_k + slot;
-      if (route_after_prev) wait_prev_layer(t);
+      if (route_after_prev) wait_input_packed(t);
       const uint8_t *expert = resolve_expert(p, la, inst);
       using W = TileWalk<FMT, GD, (GD == 16 ? 2 : 4), 1, kBuffers>;
       const uint32_t grp = lane / GD, gl = lane % GD;
