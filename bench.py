@@ -4,24 +4,33 @@
 Default workload (the config the metric is quoted
 on): a Mixtral-8x7B-shaped MoE stack, 32 layers x 8 Q4_0 experts
 (d_model 4096, d_ff 14336; 256 experts = 25.4 GB resident in HBM), top-2
-routing from N(0,1) logits per token per layer (softmax, top-2,
-renormalised), decode batch 1.  One step = one token through all 32 layers:
-layer l reads its own N(0,1) input vector x_l (standing in for the normed
-residual stream, which keeps magnitudes bounded without a norm kernel) and
-accumulates out += sum_i w_i y_i (the engine's WeightedInto accumulate).  Weights are synthetic (this library's
-counter-based generator: nibbles uniform, d = f16(U(0.005, 0.02))).
+routing from N(0,1) logits per token per layer (softmax over the selected
+two), decode batch 1.  One step = one token through all 32 layers in one
+mer_hip_moe_forward_layers launch: layer l reads its own N(0,1) input x_l
+(standing in for the normed residual stream) and accumulates
+out += sum_i w_i y_i; layer l+1 starts packing its input only after layer
+l's output is complete.  Weights come from this library's counter-based
+generator (nibbles uniform, d = f16(U(0.005, 0.02))).
 
-Prints one JSON line (rank 0).  The CPU baseline leg times the C oracle's
-restatement of the reference's Q4_0 CPU path (dequantise + f32 GEMV,
-q4_0_cpu_reference_forward) on a bounded sample of the same experts.
+--config 0: one Mixtral-shape Q4_0 expert per step (expert-FFN/s), cycling
+  over 32 distinct resident experts so no step re-reads a cached expert.
+--config 2: the Qwen3-30B-A3B shape, 48 layers x 128 Q8_0 experts
+  (d_model 2048, d_ff 768; 30.8 GB resident), top-8 from a per-layer
+  LinearGate [128 x 2048] ~ N(0, 0.02) applied to a fresh N(0,1) hidden
+  state per step and layer (routed on the host).
+
+Prints one JSON line.  The CPU baseline leg times the C oracle's
+restatement of the reference's CPU path on a bounded sample of the same
+experts: q4_0_cpu_reference_forward (dequantise + f32 GEMV) for Q4_0,
+forward_q8_0_direct_into's AVX2 kernel for Q8_0.
 """
 from __future__ import annotations
 
 import argparse
-import ctypes
 import importlib
 import json
 import os
+import re
 import sys
 import time
 
@@ -32,63 +41,74 @@ sys.path.insert(0, ROOT)
 PKG = "micro-expert-router-ssd-streamed-moe-mer_amd"
 
 HBM_PEAK_GBPS = 8000.0
-Q4_BLOCK = 18
+Q4, Q8 = 4, 5
+BLOCK_BYTES = {Q4: 18, Q8: 34}
 METRIC = "expert-FFN tokens/s + achieved HBM GB/s (% of peak), Mixtral-shape Q4_0 top-2"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_kernel_mixtral_q4_0_traffic.md")
+
+CONFIGS = {
+    0: dict(workload="mixtral-expert-q4_0", dtype=Q4, d_model=4096, d_ff=14336, layers=1, experts=32, top_k=1,
+            scale=(0.005, 0.02), metric="expert-FFN/s, one Mixtral-shape Q4_0 expert per step", unit="expert-FFN/s"),
+    1: dict(workload="mixtral-8x7b-moe-decode-q4_0-top2", dtype=Q4, d_model=4096, d_ff=14336, layers=32, experts=8,
+            top_k=2, scale=(0.005, 0.02), metric=METRIC, unit="tokens/s"),
+    2: dict(workload="qwen3-30b-a3b-moe-decode-q8_0-top8", dtype=Q8, d_model=2048, d_ff=768, layers=48, experts=128,
+            top_k=8, scale=(0.002, 0.01), metric="expert-FFN tokens/s + achieved HBM GB/s, Qwen3-30B-A3B-shape Q8_0 top-8",
+            unit="tokens/s"),
+}
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(mer, blob_dev, x_np, dm, dff, experts_per_token, budget_s, gpu_y):
+def cpu_baseline(dtype, blobs, x_np, dm, dff, experts_per_step, budget_s, gpu_y, unit, what):
     """Oracle (checker) timing on host cores: a bounded sample of expert FFNs.
 
-    Cycles through the sampled experts until `budget_s` of CPU work is
-    timed; each expert's first CPU result is also compared with the GPU's."""
+    Cycles through the sampled experts (at least 1 GiB of distinct blobs, so
+    the host's caches cannot hold the sample) until `budget_s` of CPU work
+    is timed; the first experts' CPU results are compared with the GPU's."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import mer_oracle  # noqa: E402  (test infrastructure, used as the checker)
 
     threads = max(1, min(16, os.cpu_count() or 1))
-    hosts = [blob.cpu().numpy() for blob in blob_dev]
-    times, max_err = [], 0.0
-    spent = 0.0
-    i = 0
+    hosts = [b.cpu().numpy() for b in blobs]
+    times, max_err, spent, i = [], 0.0, 0.0, 0
     while spent < budget_s or i < len(hosts):
         host = hosts[i % len(hosts)]
         t0 = time.perf_counter()
-        y = mer_oracle.q4_0_reference_forward(host, x_np, dm, dff, nthreads=threads)
+        if dtype == Q4:
+            y = mer_oracle.q4_0_reference_forward(host, x_np, dm, dff, nthreads=threads)
+        else:
+            rc, y = mer_oracle.q8_0_direct_forward(host, x_np, dm, dff, kernel=1, nthreads=threads)
+            assert rc == 0
         dt = time.perf_counter() - t0
         times.append(dt)
         spent += dt
-        if i < len(hosts):
-            err = np.abs(y.astype(np.float64) - gpu_y[i]) / (1e-3 + 1e-3 * np.abs(y))
-            max_err = max(max_err, float(err.max()))
+        if i < len(gpu_y):
+            # the parity tests' bar: |gpu - ref| <= 1e-3 |ref| + 1e-3 max(1, 1e-3 max|ref|)
+            ref = y.astype(np.float64)
+            allowed = 1e-3 * np.abs(ref) + 1e-3 * max(1.0, 1e-3 * float(np.abs(ref).max()))
+            max_err = max(max_err, float((np.abs(ref - gpu_y[i]) / allowed).max()))
         i += 1
     per_expert = float(np.mean(times))
     return {
-        "value": 1.0 / (per_expert * experts_per_token),
-        "unit": "tokens/s",
+        "value": 1.0 / (per_expert * experts_per_step),
+        "unit": unit,
         "cores": threads,
         "kind": "port",
-        "sample": (f"{len(times)} Mixtral-shape Q4_0 expert FFNs ({len(hosts)} distinct experts, cycled) with the "
-                   f"reference's q4_0_cpu_reference_forward (dequantise + f32 GEMV) restated in C on {threads} "
-                   f"threads: {spent:.1f} s, mean {per_expert * 1e3:.1f} ms/expert, scaled to "
-                   f"{experts_per_token} experts/token"),
+        "sample": (f"{len(times)} expert FFNs ({len(hosts)} distinct experts, cycled) with {what} restated in C on "
+                   f"{threads} threads: {spent:.1f} s, mean {per_expert * 1e3:.2f} ms/expert, scaled to "
+                   f"{experts_per_step} experts/step"),
         "ms_per_expert": per_expert * 1e3,
         "parity_worst_ratio": max_err,
     }
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_kernel_mixtral_q4_0_traffic.md")
-
-
-def read_traffic(dominant: str):
+def read_traffic(cfg_id: int):
     """HBM bytes per decode launch measured with rocprofv3 FETCH_SIZE and
     WRITE_SIZE passes (scaled by a copy kernel), as committed under profiles/."""
-    if dominant != "decode" or not os.path.exists(TRAFFIC_FILE):
+    if cfg_id != 1 or not os.path.exists(TRAFFIC_FILE):
         return None
-    import re
-
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", open(TRAFFIC_FILE).read())
     if not m:
         return None
@@ -100,7 +120,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
+    ap.add_argument("--layers", type=int, default=None, help="override the config's layer count")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0xC0FFEE)
@@ -122,75 +143,115 @@ def main() -> int:
     import torch
 
     mer = importlib.import_module(PKG)
+    routing = importlib.import_module(PKG + ".routing")
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     mer.init(0)
     lib = mer._lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
 
-    L, E, K, dm, dff = args.layers, 8, 2, 4096, 14336
-    ebytes = mer.expert_weight_bytes_for(dm, dff, mer.WeightDtype.Q4_0)
-    assert ebytes == 99_090_432
-    nb = ebytes // Q4_BLOCK
-    log(f"allocating {L * E} experts x {ebytes} B = {L * E * ebytes / 1e9:.2f} GB")
-    weights = torch.empty(L * E * ebytes, dtype=torch.uint8, device=dev)
-    for e in range(L * E):
-        mer.fill_synthetic(mer.WeightDtype.Q4_0, args.seed, e, nb, 0.005, 0.02, weights[e * ebytes:(e + 1) * ebytes])
+    cfg = CONFIGS[args.config]
+    dtype, dm, dff, K = cfg["dtype"], cfg["d_model"], cfg["d_ff"], cfg["top_k"]
+    L = args.layers if args.layers is not None else cfg["layers"]
+    E = cfg["experts"]
+    ebytes = mer.expert_weight_bytes_for(dm, dff, mer.WeightDtype(dtype))
+    nb = ebytes // BLOCK_BYTES[dtype]
+    n_exp = L * E
+    log(f"config {args.config}: allocating {n_exp} experts x {ebytes} B = {n_exp * ebytes / 1e9:.2f} GB")
+    weights = torch.empty(n_exp * ebytes, dtype=torch.uint8, device=dev)
+    lo, hi = cfg["scale"]
+    for e in range(n_exp):
+        mer.fill_synthetic(mer.WeightDtype(dtype), args.seed, e, nb, lo, hi, weights[e * ebytes:(e + 1) * ebytes])
     torch.cuda.synchronize()
     base = weights.data_ptr()
-    table = torch.tensor([[base + (l * E + e) * ebytes for e in range(E)] for l in range(L)],
-                         dtype=torch.int64, device=dev)
 
-    routing = importlib.import_module(PKG + ".routing")
+    def blob(e):
+        return weights[e * ebytes:(e + 1) * ebytes]
+
     total_steps = args.warmup + args.steps
-    rng = np.random.default_rng(args.seed + 2)
-    logits = rng.standard_normal((total_steps, L, E)).astype(np.float32)
-    ids = np.zeros((total_steps, L, 1, K), np.int32)
-    wts = np.zeros((total_steps, L, 1, K), np.float32)
-    for s in range(total_steps):
-        for l in range(L):
-            i, w = routing.route_scores(logits[s, l], K)
-            ids[s, l, 0], wts[s, l, 0] = i, w
-    ids_d = torch.from_numpy(ids).to(dev)
-    wts_d = torch.from_numpy(wts).to(dev)
-    xs = np.random.default_rng(args.seed + 1).standard_normal((L, 1, dm)).astype(np.float32)
-    x0 = xs[0]
-    xs_d = torch.from_numpy(xs).to(dev)
+    rng_x = np.random.default_rng(args.seed + 1)
+    rng_r = np.random.default_rng(args.seed + 2)
     out = torch.zeros((1, dm), dtype=torch.float32, device=dev)
 
-    stream = torch.cuda.current_stream().cuda_stream
-    fn = lib.mer_hip_moe_forward
+    if args.config == 0:
+        # one expert per step, cycling over E distinct resident experts
+        xs = rng_x.standard_normal((1, dm)).astype(np.float32)
+        xs_d = torch.from_numpy(xs).to(dev)
+        y = torch.empty((dm,), dtype=torch.float32, device=dev)
+        fn = lib.mer_hip_expert_forward
+        all_args = [(dtype, base + (s % E) * ebytes, ebytes, xs_d.data_ptr(), dm, dm, dff, y.data_ptr(), dm, stream)
+                    for s in range(total_steps)]
+        step_bytes = ebytes + 2 * dm * 4
+        launch_bytes = step_bytes
 
-    # Pre-bound C-ABI arguments per (step, layer): the timed loop is pure launches.
-    def step_args(s):
-        return [(4, dm, dff, 1, K, table[l].data_ptr(), E, ids_d[s, l].data_ptr(), wts_d[s, l].data_ptr(),
-                 xs_d[l].data_ptr(), out.data_ptr(), 2, stream) for l in range(L)]
-
-    # one multi-layer launch per token: prebuilt mer_layer_args arrays
-    fn_layers = lib.mer_hip_moe_forward_layers
-
-    def layer_array(s):
-        arr = (mer._lib.MerLayerArgs * L)()
-        for l in range(L):
-            arr[l] = mer._lib.MerLayerArgs(table[l].data_ptr(), E, ids_d[s, l].data_ptr(), wts_d[s, l].data_ptr(),
-                                           xs_d[l].data_ptr(), out.data_ptr())
-        return arr
-
-    if args.per_layer:
-        all_args = [step_args(s) for s in range(total_steps)]
-    else:
-        flags = 2 | (8 if args.route_after_prev else 0)  # ACCUMULATE [| ROUTE_AFTER_PREV]
-        all_args = [(4, dm, dff, L, 1, K, layer_array(s), flags, stream) for s in range(total_steps)]
-
-    def run_step(s):
-        if args.per_layer:
-            for a in all_args[s]:
-                rc = fn(*a)
-                if rc:
-                    mer.errors.raise_for_status(rc)
-        else:
-            rc = fn_layers(*all_args[s])
+        def run_step(s):
+            rc = fn(*all_args[s])
             if rc:
                 mer.errors.raise_for_status(rc)
+
+        sample_experts = list(range(min(E, 16)))
+        x_ref = xs[0]
+        experts_per_step = 1
+        routing_desc = "none (one expert per step)"
+    else:
+        table = torch.tensor([[base + (l * E + e) * ebytes for e in range(E)] for l in range(L)],
+                             dtype=torch.int64, device=dev)
+        ids = np.zeros((total_steps, L, 1, K), np.int32)
+        wts = np.zeros((total_steps, L, 1, K), np.float32)
+        if args.config == 1:
+            xs = rng_x.standard_normal((1, L, 1, dm)).astype(np.float32)   # one x_l per layer
+            logits = rng_r.standard_normal((total_steps, L, E)).astype(np.float32)
+            for s in range(total_steps):
+                for l in range(L):
+                    ids[s, l, 0], wts[s, l, 0] = routing.route_scores(logits[s, l], K)
+            routing_desc = "N(0,1) logits per token and layer, softmax over the selected top-k"
+        else:
+            xs = rng_x.standard_normal((total_steps, L, 1, dm)).astype(np.float32)  # fresh hidden state per step
+            gates = (rng_r.standard_normal((L, E, dm)) * 0.02).astype(np.float32)
+            for s in range(total_steps):
+                for l in range(L):
+                    ids[s, l, 0], wts[s, l, 0] = routing.route_linear_gate(gates[l], xs[s, l, 0], K)
+            routing_desc = "LinearGate [E x d_model] ~ N(0, 0.02) per layer on the step's hidden state (host)"
+        ids_d = torch.from_numpy(ids).to(dev)
+        wts_d = torch.from_numpy(wts).to(dev)
+        xs_d = torch.from_numpy(xs).to(dev)
+        xsel = (lambda s, l: xs_d[0, l]) if args.config == 1 else (lambda s, l: xs_d[s, l])
+        per_layer_bytes = K * ebytes + 3 * dm * 4  # distinct routed experts + x in, out read + written
+        step_bytes = L * per_layer_bytes
+        flags = 2 | (8 if args.route_after_prev else 0)  # ACCUMULATE [| ROUTE_AFTER_PREV]
+        if args.per_layer:
+            fn = lib.mer_hip_moe_forward
+            all_args = [[(dtype, dm, dff, 1, K, table[l].data_ptr(), E, ids_d[s, l].data_ptr(), wts_d[s, l].data_ptr(),
+                          xsel(s, l).data_ptr(), out.data_ptr(), 2, stream) for l in range(L)] for s in range(total_steps)]
+            launch_bytes = per_layer_bytes
+
+            def run_step(s):
+                for a in all_args[s]:
+                    rc = fn(*a)
+                    if rc:
+                        mer.errors.raise_for_status(rc)
+        else:
+            fn = lib.mer_hip_moe_forward_layers
+
+            def layer_array(s):
+                arr = (mer._lib.MerLayerArgs * L)()
+                for l in range(L):
+                    arr[l] = mer._lib.MerLayerArgs(table[l].data_ptr(), E, ids_d[s, l].data_ptr(),
+                                                   wts_d[s, l].data_ptr(), xsel(s, l).data_ptr(), out.data_ptr())
+                return arr
+
+            all_args = [(dtype, dm, dff, L, 1, K, layer_array(s), flags, stream) for s in range(total_steps)]
+            launch_bytes = step_bytes
+
+            def run_step(s):
+                rc = fn(*all_args[s])
+                if rc:
+                    mer.errors.raise_for_status(rc)
+
+        # parity sample: the experts step 0 routes to in the first layers
+        sample_experts = [l * E + int(ids[0, l, 0, i]) for l in range(L) for i in range(K)][:16]
+        x_ref = xs[0, 0, 0]
+        experts_per_step = L * K
 
     log("warmup")
     for s in range(args.warmup):
@@ -211,39 +272,44 @@ def main() -> int:
     mer.take_device_status()
     elapsed = t1 - t0
     ms_per_step = elapsed * 1e3 / args.steps
-    tokens_per_s = args.steps / elapsed
+    steps_per_s = args.steps / elapsed
 
-    # Algorithmic bytes (packed weights of each distinct expert touched + f32
-    # activations in/out).  Per launch of each stage (K experts per launch):
+    # Per-launch algorithmic bytes of each stage (packed weights of each
+    # distinct expert touched + f32 activations in/out).
     proj = ebytes // 3
-    gate_up_bytes = K * 2 * proj + dm // 32 * 100 + K * dff // 32 * 100  # weights + x digits in + h digits out
-    down_bytes = K * proj + K * dff // 32 * 100 + K * 4 * dm * 4  # weights + h digits in + 4 slice partials
-    combine_bytes = K * 4 * dm * 4 + 2 * dm * 4                   # partial slices + out read/write
-    per_layer_bytes = K * ebytes + 3 * dm * 4  # + x_l in, out read + written
-    token_bytes = L * per_layer_bytes
-    prep_bytes = dm * 4 + dm // 32 * 100 + K * 12                 # x in, digit planes out, slot pointers
-    decode_bytes = per_layer_bytes if args.per_layer else token_bytes   # one decode_kernel launch
-    stage_bytes = {"gate_up": gate_up_bytes, "down": down_bytes, "combine": combine_bytes, "prep": prep_bytes,
-                   "decode": decode_bytes}
+    stage_bytes = {
+        "decode": launch_bytes,                                       # the persistent decode kernel
+        "gate_up": K * 2 * proj + dm // 32 * 100 + K * dff // 32 * 100,
+        "down": K * proj + K * dff // 32 * 100 + K * 4 * dm * 4,
+        "combine": K * 4 * dm * 4 + 2 * dm * 4,
+        "prep": dm * 4 + dm // 32 * 100 + K * 12,
+    }
     stage_info = {}
     for name, (ms, cnt) in stages.items():
         if cnt:
             avg = ms / cnt
-            stage_info[name] = {"avg_us": avg * 1e3, "launches": cnt,
-                                "gbps": stage_bytes[name] / (avg * 1e-3) / 1e9}
+            stage_info[name] = {"avg_us": avg * 1e3, "launches": cnt, "gbps": stage_bytes[name] / (avg * 1e-3) / 1e9}
     dominant = max(stage_info, key=lambda k: stage_info[k]["avg_us"] * stage_info[k]["launches"])
     dom = stage_info[dominant]
 
-    # Parity of the sampled experts: GPU single-expert forward on x0.
-    sample = [(0, l, int(ids[0, l, 0, i])) for l in range(min(L, 8)) for i in range(K)]
-    blobs = [weights[(l * E + e) * ebytes:(l * E + e + 1) * ebytes] for _, l, e in sample]
-    xdev = torch.from_numpy(x0[0]).to(dev)
-    gpu_y = [mer.q4_0_forward(b, xdev, dm, dff).cpu().numpy().astype(np.float64) for b in blobs]
+    # GPU outputs of the sampled experts on the reference input (parity leg)
+    xdev = torch.from_numpy(np.ascontiguousarray(x_ref)).to(dev)
+    gpu_y = [mer.dispatch_expert_forward(mer.WeightDtype(dtype), blob(e), xdev, dm, dff).cpu().numpy().astype(np.float64)
+             for e in sample_experts]
 
+    config = {"workload": cfg["workload"], "layers": L, "experts_per_layer": E if args.config else 1,
+              "top_k": K, "d_model": dm, "d_ff": dff, "weights": "Q4_0" if dtype == Q4 else "Q8_0", "batch": 1,
+              "resident_bytes": n_exp * ebytes, "bytes_per_step": step_bytes, "parallelism": "single-gpu",
+              "routing": routing_desc}
+    if args.config:
+        config["launch"] = "per-layer" if args.per_layer else "all-layers"
+        config["routing_use"] = ("each layer's routing used only after the previous layer's output is complete"
+                                 if args.per_layer or args.route_after_prev else
+                                 "every layer's routing is a launch input")
     result = {
-        "metric": METRIC,
-        "value": tokens_per_s,
-        "unit": "tokens/s",
+        "metric": cfg["metric"],
+        "value": steps_per_s,
+        "unit": cfg["unit"],
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -253,23 +319,16 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "mixtral-8x7b-moe-decode-q4_0-top2", "layers": L, "experts_per_layer": E,
-                   "top_k": K, "d_model": dm, "d_ff": dff, "batch": 1, "resident_bytes": L * E * ebytes,
-                   "bytes_per_token": token_bytes, "parallelism": "single-gpu",
-                   "launch": "per-layer" if args.per_layer else "all-layers",
-                   "routing": ("each layer's routing used only after the previous layer's output is complete"
-                               if args.per_layer or args.route_after_prev else
-                               "every layer's routing is a launch input (exogenous N(0,1) logits)")},
-        "hbm_gbps": token_bytes * tokens_per_s / 1e9,
-        "hbm_frac_of_peak": token_bytes * tokens_per_s / 1e9 / HBM_PEAK_GBPS,
+        "config": config,
+        "hbm_gbps": step_bytes * steps_per_s / 1e9,
+        "hbm_frac_of_peak": step_bytes * steps_per_s / 1e9 / HBM_PEAK_GBPS,
         "roofline": {"bound": "hbm", "kernel": "decode_kernel" if dominant == "decode" else f"proj_kernel ({dominant})",
-                     "achieved": dom["gbps"],
-                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": dom["gbps"] / HBM_PEAK_GBPS,
-                     "traffic": None, "algorithmic_bytes_per_launch": stage_bytes[dominant],
-                     "avg_launch_us": dom["avg_us"]},
+                     "achieved": dom["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": dom["gbps"] / HBM_PEAK_GBPS, "traffic": None,
+                     "algorithmic_bytes_per_launch": stage_bytes[dominant], "avg_launch_us": dom["avg_us"]},
         "stages": stage_info,
     }
-    traffic = read_traffic(dominant)
+    traffic = read_traffic(args.config) if dominant == "decode" and not args.per_layer else None
     if traffic is not None:
         result["roofline"]["traffic"] = traffic["bytes"]
         result["roofline"]["traffic_source"] = traffic["source"]
@@ -283,7 +342,12 @@ def main() -> int:
         log(f"copy calibration: 3 launches of add(src, 1) over {args.copy_calibration} MiB in, same out")
     if not args.no_cpu_baseline:
         log("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(mer, blobs, x0[0], dm, dff, L * K, args.cpu_seconds, gpu_y)
+        what = ("the reference's q4_0_cpu_reference_forward (dequantise + f32 GEMV)" if dtype == Q4 else
+                "the reference's forward_q8_0_direct_into AVX2 row kernels")
+        n_cpu = max(len(sample_experts), min(n_exp, -(-(1 << 30) // ebytes)))
+        cpu_experts = sample_experts + [e for e in range(n_exp) if e not in sample_experts][:n_cpu - len(sample_experts)]
+        result["cpu_baseline"] = cpu_baseline(dtype, [blob(e) for e in cpu_experts], x_ref, dm, dff,
+                                              experts_per_step, args.cpu_seconds, gpu_y, cfg["unit"], what)
     print(json.dumps(result), flush=True)
     return 0
 
