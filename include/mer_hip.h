@@ -214,6 +214,38 @@ typedef struct mer_layer_args {
 int mer_hip_moe_forward_layers(int dtype, size_t d_model, size_t d_ff, size_t n_layers, size_t n_tokens,
                                size_t top_k, const mer_layer_args *layers, unsigned flags, void *stream);
 
+/* ---- routing -------------------------------------------------------- */
+/* Options of the LinearGate routing surface (LinearGate::with_routing,
+ * gating.rs:207-268).  NULL options = LinearGate::new: softmax scoring,
+ * renormalised top-k, no bias, no groups, unit scaling. */
+typedef struct mer_gate_options {
+  int32_t scoring;              /* 0 = softmax, 1 = sigmoid (ScoringFunc)   */
+  int32_t normalise_topk;       /* nonzero: divide the top-k weights by     */
+                                /* their sum when it is finite and > 0      */
+  const float *correction_bias; /* device [n_experts], added to selection   */
+                                /* scores only; NULL = none                 */
+  uint32_t n_group;             /* group-limited selection (n_group,        */
+  uint32_t topk_group;          /* topk_group); n_group <= 1 disables it    */
+  float routed_scaling_factor;  /* applied to the final weights if != 1     */
+} mer_gate_options;
+
+#define MER_MAX_ROUTER_EXPERTS 1024
+#define MER_MAX_ROUTER_TOP_K 64
+
+/* LinearGate::route_with_scratch (gating.rs:395-476) for n_tokens hidden
+ * states on the device: logits = W x, scores, optional bias and group
+ * filter, deterministic top-k (higher score first, lower id on ties),
+ * weights = unbiased scores renormalised and scaled.
+ *   d_gate[n_experts * d_model] (row-major f32), d_x[n_tokens * d_model];
+ *   d_ids / d_weights [n_tokens * top_k]: slots beyond the experts with a
+ *   finite score get id -1 and weight 0 (the routed forwards skip them);
+ *   d_logits [n_tokens * n_experts] or NULL.
+ * n_experts <= MER_MAX_ROUTER_EXPERTS, top_k <= MER_MAX_ROUTER_TOP_K,
+ * d_model <= MER_MAX_EXPERT_DIM. */
+int mer_hip_route_linear_gate(const float *d_gate, size_t n_experts, size_t d_model, const float *d_x,
+                              size_t n_tokens, size_t top_k, const mer_gate_options *options, int32_t *d_ids,
+                              float *d_weights, float *d_logits, void *stream);
+
 /* Synthetic bench / test data: fill n_blocks GGUF blocks of expert
  * `expert_index` starting at block `block_begin` with this library's
  * counter-based generator (nibbles / int8 uniform, d = f16(U(lo,hi))). */

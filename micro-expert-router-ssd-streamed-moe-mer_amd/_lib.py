@@ -30,6 +30,18 @@ class MerLayerArgs(ctypes.Structure):
     ]
 
 
+class MerGateOptions(ctypes.Structure):
+    """mer_gate_options (LinearGate::with_routing, gating.rs:207-268)."""
+    _fields_ = [
+        ("scoring", ctypes.c_int32),
+        ("normalise_topk", ctypes.c_int32),
+        ("correction_bias", ctypes.c_void_p),
+        ("n_group", ctypes.c_uint32),
+        ("topk_group", ctypes.c_uint32),
+        ("routed_scaling_factor", ctypes.c_float),
+    ]
+
+
 class MerErrorInfo(ctypes.Structure):
     _fields_ = [
         ("status", ctypes.c_int32),
@@ -87,6 +99,9 @@ SIGNATURES = {
                 ctypes.c_uint, c_void]),
     "mer_hip_moe_forward_layers": (
         c_int, [c_int, c_size, c_size, c_size, c_size, c_size, ctypes.POINTER(MerLayerArgs), ctypes.c_uint, c_void]),
+    "mer_hip_route_linear_gate": (
+        c_int, [c_void, c_size, c_size, c_void, c_size, c_size, ctypes.POINTER(MerGateOptions), c_void, c_void, c_void,
+                c_void]),
     "mer_hip_fill_synthetic": (
         c_int, [c_int, c_u64, c_u64, c_u64, c_u64, c_float, c_float, c_void, c_void]),
 }

@@ -420,6 +420,7 @@ int run_experts(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
   q.table = table;
   q.table_len = table_len;
   q.ids = ids;
+  q.weights = weights;
   q.single = single;
   q.top_k = top_k;
   q.inst_ptr = inst_ptr;
@@ -790,6 +791,52 @@ int mer_hip_moe_forward_layers(int dtype, size_t d_model, size_t d_ff, size_t n_
   }
   return run_decode(dtype, d_model, d_ff, (uint32_t)n_layers, (uint32_t)n_tokens, (uint32_t)top_k, la, nullptr,
                     flags, (hipStream_t)stream);
+}
+
+int mer_hip_route_linear_gate(const float *d_gate, size_t n_experts, size_t d_model, const float *d_x,
+                              size_t n_tokens, size_t top_k, const mer_gate_options *options, int32_t *d_ids,
+                              float *d_weights, float *d_logits, void *stream) {
+  int rc = require_init();
+  if (rc) return rc;
+  if (n_tokens == 0) return MER_OK;
+  if (!d_gate || !d_x || !d_ids || !d_weights) return fail(MER_ERR_INVALID_LAYOUT, "null router buffer");
+  if (n_experts == 0 || n_experts > kMaxRouterExperts)
+    return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "router supports 1..%u experts, got %zu", kMaxRouterExperts, n_experts);
+  if (top_k == 0 || top_k > n_experts || top_k > kMaxRouterTopK)
+    return fail(MER_ERR_INVALID_LAYOUT, "top_k must be in 1..=min(n_experts, %u), got %zu", kMaxRouterTopK, top_k);
+  if (d_model == 0 || d_model > MER_MAX_EXPERT_DIM)
+    return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "router d_model must be in 1..=%d, got %zu", MER_MAX_EXPERT_DIM, d_model);
+  if (n_tokens > (1u << 30)) return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "too many tokens");
+  RouterParams p{};
+  p.gate = d_gate;
+  p.x = d_x;
+  p.ids = d_ids;
+  p.weights = d_weights;
+  p.logits = d_logits;
+  p.n_experts = (uint32_t)n_experts;
+  p.d_model = (uint32_t)d_model;
+  p.n_tokens = (uint32_t)n_tokens;
+  p.top_k = (uint32_t)top_k;
+  p.scoring = 0;
+  p.normalise = 1;
+  p.n_group = 1;
+  p.topk_group = 1;
+  p.scaling = 1.0f;
+  if (options) {
+    if (options->scoring != 0 && options->scoring != 1)
+      return fail(MER_ERR_INVALID_LAYOUT, "unknown scoring function %d", options->scoring);
+    if (options->n_group > kMaxRouterGroups)
+      return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "router supports at most %u groups", kMaxRouterGroups);
+    p.scoring = options->scoring;
+    p.normalise = options->normalise_topk != 0;
+    p.bias = options->correction_bias;
+    p.n_group = options->n_group;
+    p.topk_group = options->topk_group;
+    p.scaling = options->routed_scaling_factor;
+  }
+  hipError_t e = launch_router(p, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "router launch");
+  return MER_OK;
 }
 
 int mer_hip_fill_synthetic(int dtype, uint64_t seed, uint64_t expert_index, uint64_t block_begin, uint64_t n_blocks,

@@ -401,9 +401,13 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       // zero expert, so nothing waits on this item.)
       const uint32_t t = j;
       if (route_after_prev) wait_prev_layer(t);
+      // A zero-weight slot is skipped by the combine (engine.rs:5575-5580),
+      // so its id is not checked (the router marks unused slots id -1, w 0).
       if (lane < p.top_k && !p.single) {
         const int32_t id = la.ids[t * p.top_k + lane];
-        if (id < 0 || (uint32_t)id >= la.table_len || !la.table[id]) set_status(p, 16u /* MER_ERR_RESIDENCY_MISS */);
+        const bool unused = la.weights && la.weights[t * p.top_k + lane] == 0.0f;
+        if (!unused && (id < 0 || (uint32_t)id >= la.table_len || !la.table[id]))
+          set_status(p, 16u /* MER_ERR_RESIDENCY_MISS */);
       }
     } else if (j < p.off_g) {
       // ---- P: pack part of the token's layer input ------------------------

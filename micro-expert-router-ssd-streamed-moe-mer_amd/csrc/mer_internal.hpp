@@ -20,6 +20,7 @@ struct PrepParams {
   const void *const *table;  // expert table (device), or null with `single`
   uint32_t table_len;
   const int32_t *ids;        // [n_tokens * top_k]
+  const float *weights;      // [n_tokens * top_k] slot weights, or null
   const uint8_t *single;     // single expert blob (overrides table / ids)
   uint32_t top_k;
   const uint8_t **inst_ptr;  // out: [n_tokens * top_k]
@@ -128,6 +129,27 @@ struct DecodeParams {
   uint64_t *trace;           // optional item trace [trace_cap][4], or null
   uint64_t trace_cap;
 };
+
+// ---- LinearGate router (mer_router.hip) -----------------------------------
+constexpr uint32_t kMaxRouterExperts = 1024;
+constexpr uint32_t kMaxRouterTopK = 64;
+constexpr uint32_t kMaxRouterGroups = 64;
+
+struct RouterParams {
+  const float *gate;    // [n_experts][d_model]
+  const float *x;       // [n_tokens][d_model]
+  const float *bias;    // [n_experts] selection-only correction bias, or null
+  int32_t *ids;         // [n_tokens][top_k]; -1 where fewer experts qualify
+  float *weights;       // [n_tokens][top_k]; 0 where fewer experts qualify
+  float *logits;        // [n_tokens][n_experts], or null
+  uint32_t n_experts, d_model, n_tokens, top_k;
+  int32_t scoring;      // 0 softmax, 1 sigmoid
+  int32_t normalise;    // renormalise the top-k weights
+  uint32_t n_group, topk_group;
+  float scaling;        // routed scaling factor
+};
+
+hipError_t launch_router(const RouterParams &p, hipStream_t st);
 
 const void *decode_kernel_fn(int fmt, int gg, int gd);
 hipError_t launch_decode(const void *fn, uint32_t grid, const DecodeParams &p, hipStream_t st);

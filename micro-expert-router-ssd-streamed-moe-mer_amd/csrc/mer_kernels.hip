@@ -90,7 +90,8 @@ __device__ __forceinline__ void pack_vector(const float *x, uint32_t nblocks, ui
 
 // One workgroup per token: pack x[t] (fast path only) and resolve the blob
 // pointer of each of the token's expert slots.  An id outside the table or
-// a non-resident entry resolves to null and records a residency miss.
+// a non-resident entry resolves to null and records a residency miss,
+// except in a zero-weight slot, which the combine skips (engine.rs:5575-5580).
 template <int FMT>
 __global__ __launch_bounds__(256) void prep_kernel(PrepParams q) {
   const uint32_t t = blockIdx.x;
@@ -99,11 +100,12 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepParams q) {
     const uint8_t *ptr = q.single;
     if (!ptr) {
       const int32_t id = q.ids[inst];
+      const bool unused = q.weights && q.weights[inst] == 0.0f;
       if (id < 0 || (uint32_t)id >= q.table_len) {
-        record_status(16u /* MER_ERR_RESIDENCY_MISS */);
+        if (!unused) record_status(16u /* MER_ERR_RESIDENCY_MISS */);
       } else {
         ptr = reinterpret_cast<const uint8_t *>(q.table[id]);
-        if (!ptr) record_status(16u);
+        if (!ptr && !unused) record_status(16u);
       }
     }
     q.inst_ptr[inst] = ptr;

@@ -118,3 +118,35 @@ class SkewedStream:
             r += 1
         self.prev = list(chosen)
         return chosen
+
+
+def route_linear_gate_gpu(gate, x, top_k: int, *, sigmoid: bool = False, normalise: bool = True, bias=None,
+                          n_group: int = 1, topk_group: int = 1, scaling: float = 1.0, return_logits: bool = False):
+    """LinearGate::route_with_scratch (gating.rs:395-476) on the GPU through
+    mer_hip_route_linear_gate.  gate: f32 [n_experts, d_model] and x: f32
+    [n_tokens, d_model] device tensors; returns device tensors ids (int32,
+    -1 for slots no expert qualifies for), weights (f32) [n_tokens, top_k]
+    and, when asked, the logits [n_tokens, n_experts]."""
+    import ctypes
+
+    import torch
+
+    from . import _lib, errors
+    from .expert import _init_for, _ptr, _stream
+
+    if gate.dim() != 2 or x.dim() != 2 or gate.shape[1] != x.shape[1]:
+        raise ValueError("gate must be [n_experts, d_model] and x [n_tokens, d_model]")
+    _init_for(x)
+    n_experts, d_model = gate.shape
+    n_tokens = x.shape[0]
+    ids = torch.empty((n_tokens, top_k), dtype=torch.int32, device=x.device)
+    weights = torch.empty((n_tokens, top_k), dtype=torch.float32, device=x.device)
+    logits = torch.empty((n_tokens, n_experts), dtype=torch.float32, device=x.device) if return_logits else None
+    opts = _lib.MerGateOptions(1 if sigmoid else 0, 1 if normalise else 0,
+                               0 if bias is None else _ptr(bias, torch.float32), n_group, topk_group, scaling)
+    rc = _lib.lib().mer_hip_route_linear_gate(_ptr(gate, torch.float32), n_experts, d_model, _ptr(x, torch.float32),
+                                              n_tokens, top_k, ctypes.byref(opts), ids.data_ptr(), weights.data_ptr(),
+                                              0 if logits is None else logits.data_ptr(), _stream())
+    if rc:
+        errors.raise_for_status(rc)
+    return (ids, weights, logits) if return_logits else (ids, weights)

@@ -807,6 +807,124 @@ void mo_topk_softmax_logits(const float *logits, size_t n, size_t top_k,
   free(s);
 }
 
+/* gating.rs:395-476 route_with_scratch, full routing surface
+ * (LinearGate::with_routing, gating.rs:207-268):
+ *   scores    = softmax(logits) (transformer.rs:2807) or 1/(1+exp(-l))
+ *               (gating.rs:271-279);
+ *   selection = scores + correction_bias (if any);
+ *   optional group filter (gating.rs:332-370): n_group groups of
+ *               n/n_group experts scored by the sum of their two best
+ *               selection scores (the second only if finite), the best
+ *               topk_group groups (score desc by total order, id asc)
+ *               survive; disabled unless 1 < topk_group < n_group and
+ *               n % n_group == 0 (group_filter_shape, :321-331);
+ *   top-k over surviving experts with finite selection scores
+ *               (insert_top_expert, :296-320);
+ *   weights   = the unbiased scores at the chosen experts, divided by
+ *               their (sequential f32) sum when normalise and the sum is
+ *               finite and > 0, then multiplied by the routed scaling
+ *               factor when it is finite and != 1.
+ * pinned by: test_oracle_golden.py (the reference's gating.rs tests:
+ * identity-gate sigmoid / bias / group / scaling / tie cases). */
+size_t mo_gate_route_ex(const float *logits, size_t n, size_t top_k,
+                        int scoring, int normalise, const float *bias,
+                        size_t n_group, size_t topk_group, float scaling,
+                        uint32_t *ids, float *weights) {
+  float *scores = (float *)malloc(sizeof(float) * (n ? n : 1));
+  float *selection = (float *)malloc(sizeof(float) * (n ? n : 1));
+  uint32_t *gids = (uint32_t *)malloc(sizeof(uint32_t) * (n_group ? n_group : 1));
+  float *gsel = (float *)malloc(sizeof(float) * (n_group ? n_group : 1));
+  float *tsel = (float *)malloc(sizeof(float) * (top_k ? top_k : 1));
+  memcpy(scores, logits, sizeof(float) * n);
+  if (scoring == 0) {
+    mo_softmax_inplace(scores, n);
+  } else {
+    for (size_t e = 0; e < n; ++e) scores[e] = 1.0f / (1.0f + expf(-scores[e]));
+  }
+  for (size_t e = 0; e < n; ++e) selection[e] = bias ? scores[e] + bias[e] : scores[e];
+  size_t group_size = 0, n_sel_groups = 0;
+  if (n_group > 1 && topk_group > 0 && topk_group < n_group && n % n_group == 0) {
+    group_size = n / n_group;
+    float *gscore = (float *)malloc(sizeof(float) * n_group);
+    for (size_t g = 0; g < n_group; ++g) {
+      float top1 = -INFINITY, top2 = -INFINITY;
+      for (size_t i = 0; i < group_size; ++i) {
+        float v = selection[g * group_size + i];
+        if (v > top1) {
+          top2 = top1;
+          top1 = v;
+        } else if (v > top2) {
+          top2 = v;
+        }
+      }
+      gscore[g] = top1 + (isfinite(top2) ? top2 : 0.0f);
+    }
+    /* insert_top_group: total order, lower id on ties, non-finite kept */
+    size_t c = 0;
+    for (size_t g = 0; g < n_group; ++g) {
+      size_t pos = c;
+      for (size_t i = 0; i < c; ++i) {
+        int32_t a = total_key(gscore[g]), b = total_key(gsel[i]);
+        if (a > b || (a == b && g < gids[i])) {
+          pos = i;
+          break;
+        }
+      }
+      if (pos == c && c >= topk_group) continue;
+      size_t last = c < topk_group ? c : topk_group - 1;
+      for (size_t i = last; i > pos; --i) {
+        gids[i] = gids[i - 1];
+        gsel[i] = gsel[i - 1];
+      }
+      gids[pos] = (uint32_t)g;
+      gsel[pos] = gscore[g];
+      if (c < topk_group) c++;
+    }
+    n_sel_groups = c;
+    free(gscore);
+    /* experts of groups that did not survive cannot be selected */
+    for (size_t e = 0; e < n; ++e) {
+      int allowed = 0;
+      for (size_t i = 0; i < n_sel_groups; ++i)
+        if (gids[i] == e / group_size) allowed = 1;
+      if (!allowed) selection[e] = NAN; /* skipped as non-finite below */
+    }
+  }
+  size_t cnt = 0;
+  topk_select(selection, n, top_k, ids, tsel, &cnt);
+  float sum = 0.0f;
+  for (size_t i = 0; i < cnt; ++i) {
+    weights[i] = scores[ids[i]];
+    sum = sum + weights[i];
+  }
+  if (normalise && isfinite(sum) && sum > 0.0f)
+    for (size_t i = 0; i < cnt; ++i) weights[i] = weights[i] / sum;
+  if (scaling != 1.0f && isfinite(scaling))
+    for (size_t i = 0; i < cnt; ++i) weights[i] = weights[i] * scaling;
+  free(scores);
+  free(selection);
+  free(gids);
+  free(gsel);
+  free(tsel);
+  return cnt;
+}
+
+/* logits = W x (dot_f32 order), then mo_gate_route_ex. */
+size_t mo_linear_gate_route_ex(const float *w, size_t num_experts, size_t d_model,
+                               const float *x, size_t top_k, int scoring,
+                               int normalise, const float *bias, size_t n_group,
+                               size_t topk_group, float scaling, uint32_t *ids,
+                               float *weights, float *logits_out) {
+  float *logits = (float *)malloc(sizeof(float) * (num_experts ? num_experts : 1));
+  for (size_t e = 0; e < num_experts; ++e)
+    logits[e] = dot_f32(w + e * d_model, x, d_model);
+  if (logits_out) memcpy(logits_out, logits, sizeof(float) * num_experts);
+  size_t c = mo_gate_route_ex(logits, num_experts, top_k, scoring, normalise, bias,
+                              n_group, topk_group, scaling, ids, weights);
+  free(logits);
+  return c;
+}
+
 /* ------------------------------------------------------------------ */
 /* workload.rs:54-175 SkewedStream. */
 struct mo_skewed_stream {

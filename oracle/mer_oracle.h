@@ -103,6 +103,17 @@ void mo_softmax_inplace(float *v, size_t n);
 int mo_linear_gate_route(const float *w, size_t num_experts, size_t d_model,
                          const float *x, size_t top_k, uint32_t *ids,
                          float *weights);
+/* Full LinearGate routing surface (gating.rs:207-476): scoring 0 = softmax,
+ * 1 = sigmoid; bias may be NULL; returns the number of experts chosen. */
+size_t mo_gate_route_ex(const float *logits, size_t n, size_t top_k,
+                        int scoring, int normalise, const float *bias,
+                        size_t n_group, size_t topk_group, float scaling,
+                        uint32_t *ids, float *weights);
+size_t mo_linear_gate_route_ex(const float *w, size_t num_experts, size_t d_model,
+                               const float *x, size_t top_k, int scoring,
+                               int normalise, const float *bias, size_t n_group,
+                               size_t topk_group, float scaling, uint32_t *ids,
+                               float *weights, float *logits_out);
 void mo_topk_softmax_logits(const float *logits, size_t n, size_t top_k,
                             uint32_t *ids, float *weights);
 

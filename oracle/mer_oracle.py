@@ -55,6 +55,10 @@ _SIG = {
     "mo_softmax_inplace": (None, [_f32p, _sz]),
     "mo_linear_gate_route": (ctypes.c_int, [_f32p, _sz, _sz, _f32p, _sz, _u32p, _f32p]),
     "mo_topk_softmax_logits": (None, [_f32p, _sz, _sz, _u32p, _f32p]),
+    "mo_gate_route_ex": (_sz, [_f32p, _sz, _sz, ctypes.c_int, ctypes.c_int, _f32p, _sz, _sz, ctypes.c_float,
+                               _u32p, _f32p]),
+    "mo_linear_gate_route_ex": (_sz, [_f32p, _sz, _sz, _f32p, _sz, ctypes.c_int, ctypes.c_int, _f32p, _sz, _sz,
+                                      ctypes.c_float, _u32p, _f32p, _f32p]),
     "mo_skewed_new": (ctypes.c_void_p, [ctypes.c_uint32, _sz, ctypes.c_double, ctypes.c_double, ctypes.c_uint64]),
     "mo_skewed_next": (_sz, [ctypes.c_void_p, _u32p]),
     "mo_skewed_free": (None, [ctypes.c_void_p]),
@@ -264,6 +268,34 @@ def topk_softmax_logits(logits, top_k: int) -> tuple[np.ndarray, np.ndarray]:
     ws = np.zeros(top_k, np.float32)
     lib().mo_topk_softmax_logits(_f(la), la.size, top_k, _u32(ids), _f(ws))
     return ids, ws
+
+
+def gate_route_ex(logits, top_k: int, *, sigmoid: bool = False, normalise: bool = True, bias=None,
+                  n_group: int = 1, topk_group: int = 1, scaling: float = 1.0) -> tuple[np.ndarray, np.ndarray]:
+    """LinearGate scoring + selection (gating.rs:395-476) on given logits."""
+    la = np.ascontiguousarray(logits, np.float32)
+    ba = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    ids = np.zeros(max(top_k, 1), np.uint32)
+    ws = np.zeros(max(top_k, 1), np.float32)
+    n = lib().mo_gate_route_ex(_f(la), la.size, top_k, int(sigmoid), int(normalise), None if ba is None else _f(ba),
+                               n_group, topk_group, scaling, _u32(ids), _f(ws))
+    return ids[:n], ws[:n]
+
+
+def linear_gate_route_ex(w: np.ndarray, x: np.ndarray, top_k: int, **opts) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """logits = W x (dot_f32 order), then gate_route_ex; also returns the logits."""
+    wa = np.ascontiguousarray(w, np.float32)
+    xa = np.ascontiguousarray(x, np.float32)
+    bias = opts.get("bias")
+    ba = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    ids = np.zeros(max(top_k, 1), np.uint32)
+    ws = np.zeros(max(top_k, 1), np.float32)
+    lo = np.zeros(wa.shape[0], np.float32)
+    n = lib().mo_linear_gate_route_ex(_f(wa), wa.shape[0], wa.shape[1], _f(xa), top_k, int(opts.get("sigmoid", False)),
+                                      int(opts.get("normalise", True)), None if ba is None else _f(ba),
+                                      opts.get("n_group", 1), opts.get("topk_group", 1), opts.get("scaling", 1.0),
+                                      _u32(ids), _f(ws), _f(lo))
+    return ids[:n], ws[:n], lo
 
 
 class SkewedStream:

@@ -450,3 +450,59 @@ def test_skewed_stream_properties(oracle):
         return n
 
     assert repeats(0.9) > 3 * repeats(0.0)
+
+
+def test_gate_routing_surface_known_answers(oracle):
+    """The reference's own LinearGate tests with an identity gate (logit[i] =
+    x[i]): sigmoid scoring, selection-only bias, group-limited selection,
+    routed scaling and the default softmax gate."""
+    g = GOLDEN["gate_routing_surface_known_answers"]
+    for c in g["cases"]:
+        w = np.eye(c["n"], dtype=np.float32)
+        ids, ws, _ = oracle.linear_gate_route_ex(w, np.array(c["x"], np.float32), c["top_k"], sigmoid=c["sigmoid"],
+                                                 normalise=c["normalise"], bias=c["bias"], n_group=c["n_group"],
+                                                 topk_group=c["topk_group"], scaling=c["scaling"])
+        if "experts" in c:
+            assert list(ids) == c["experts"], c["name"]
+        if "weights" in c:
+            assert np.allclose(ws, c["weights"], atol=c["weight_tol"]), c["name"]
+        if "weight_sum" in c:
+            assert abs(float(ws.sum()) - c["weight_sum"]) < c["weight_tol"], c["name"]
+        if "experts_min" in c:
+            assert len(ids) == c["count"] and all(int(e) >= c["experts_min"] for e in ids), c["name"]
+    t = g["ties"]
+    ids, ws, _ = oracle.linear_gate_route_ex(np.zeros((t["num_experts"], t["d_model"]), np.float32),
+                                             np.array(t["x"], np.float32), t["top_k"])
+    assert list(ids) == t["experts"] and np.allclose(ws, t["weight"], atol=1e-6)
+
+
+def test_gate_route_ex_default_equals_default_gate(oracle):
+    """With the default options the full routing surface is the default
+    gate (pinned above by its own known answers)."""
+    rng = np.random.default_rng(12)
+    for _ in range(50):
+        w = rng.standard_normal((16, 24)).astype(np.float32)
+        x = rng.standard_normal(24).astype(np.float32)
+        ids0, ws0 = oracle.linear_gate_route(w, x, 4)
+        ids1, ws1, _ = oracle.linear_gate_route_ex(w, x, 4)
+        assert list(ids0) == list(ids1) and np.array_equal(ws0, ws1)
+
+
+def test_gate_group_filter_brute_force(oracle):
+    """Group-limited selection against brute force on small cases: the
+    chosen experts are the top-k (score desc, id asc) among the experts of
+    the topk_group groups with the largest top-2 sums."""
+    rng = np.random.default_rng(13)
+    for _ in range(200):
+        n, n_group, topk_group, k = 16, 4, 2, 3
+        logits = rng.standard_normal(n).astype(np.float32)
+        bias = rng.standard_normal(n).astype(np.float32) * 0.5
+        ids, _ = oracle.gate_route_ex(logits, k, sigmoid=True, normalise=False, bias=bias, n_group=n_group,
+                                      topk_group=topk_group)
+        sel = (1.0 / (1.0 + np.exp(-logits.astype(np.float64)))) + bias
+        gs = n // n_group
+        gsum = [sorted(sel[g * gs:(g + 1) * gs])[-1] + sorted(sel[g * gs:(g + 1) * gs])[-2] for g in range(n_group)]
+        groups = sorted(range(n_group), key=lambda g: (-gsum[g], g))[:topk_group]
+        cand = [e for e in range(n) if e // gs in groups]
+        want = sorted(cand, key=lambda e: (-sel[e], e))[:k]
+        assert list(ids) == want
