@@ -254,6 +254,66 @@ int mer_hip_fill_synthetic(int dtype, uint64_t seed, uint64_t expert_index,
                            float scale_lo, float scale_hi, void *d_dst,
                            void *stream);
 
+/* ---- VRAM expert-slot cache (RAM -> VRAM tier) --------------------------
+ * Replaces the physical VRAM registry of the GPU backend
+ * (backend/mod.rs:548-1047: PhysicalGpuExpertRegistry, generation-keyed
+ * lookup at :709-741, LRU eviction at :826-840) and the upload half of
+ * GpuExpertCache admission (expert_cache.rs:1281-1340).
+ *
+ * A cache owns an arena of n_slots expert-sized slots in VRAM (expert size
+ * = mer_expert_weight_bytes(dtype, d_model, d_ff)), a device table of
+ * n_experts pointers (null = not resident) and a copy stream of its own.
+ * The table is the expert_table of mer_hip_moe_forward and of
+ * mer_layer_args (table_len = n_experts).
+ *
+ * prepare(ids, generations, host_blobs, n, stream): makes all n experts
+ * resident for the work the caller enqueues next on `stream` (its compute
+ * stream).  For each id: a stored entry of the same generation is a hit
+ * (LRU touch); a newer stored generation fails the call with
+ * MER_ERR_RESIDENCY_MISS and changes nothing; an older one is retired and
+ * the expert is uploaded from host_blobs[i] (expert-sized; allocate it with
+ * mer_hip_host_alloc so the copy overlaps compute) into a free slot or the
+ * least recently used slot that this call does not need.  Uploads run on
+ * the cache's copy stream; `stream` waits for them (events, no host wait)
+ * and then the table entries are written on `stream`.  generations may be
+ * NULL (all 0); host_blobs may be NULL or hold NULL for ids known to be
+ * resident.  More distinct ids than slots fails with
+ * MER_ERR_PHYSICAL_CAPACITY before anything changes.
+ *
+ * prefetch(...): starts the uploads of misses without making any stream
+ * wait and without publishing them (a later prepare does); it never evicts
+ * the slots of the last prepare, and ids beyond what then fits are dropped
+ * (a prefetch is a hint).  Use it for the predicted experts of the
+ * next step (the engine's prefetch hook, engine.rs:5287-5322).
+ *
+ * A slot is overwritten only after the compute that used it: every prepare
+ * and prefetch first records, on `stream`, that the work enqueued there so
+ * far may use the last prepare's slots; release() records the same point
+ * explicitly (for callers whose compute runs on another stream).  Calls on
+ * one cache are serialised by a mutex; `stream` must be the compute stream
+ * that uses the table. */
+typedef struct mer_slot_cache mer_slot_cache;
+typedef struct mer_slot_stats {
+  uint64_t hits, misses, prefetches, evictions, stale_retirements;
+  uint64_t bytes_uploaded;
+  uint64_t resident; /* slots holding an expert now */
+} mer_slot_stats;
+int mer_slot_cache_create(int dtype, size_t d_model, size_t d_ff, size_t n_slots, size_t n_experts,
+                          mer_slot_cache **out);
+int mer_slot_cache_destroy(mer_slot_cache *cache);
+const void *const *mer_slot_cache_table(mer_slot_cache *cache);
+int mer_slot_cache_prepare(mer_slot_cache *cache, const uint32_t *ids, const uint64_t *generations,
+                           const void *const *host_blobs, size_t n, void *stream);
+int mer_slot_cache_prefetch(mer_slot_cache *cache, const uint32_t *ids, const uint64_t *generations,
+                            const void *const *host_blobs, size_t n, void *stream);
+int mer_slot_cache_release(mer_slot_cache *cache, void *stream);
+int mer_slot_cache_stats(mer_slot_cache *cache, mer_slot_stats *out);
+/* Pinned (page-locked) host memory for expert bytes that feed the cache:
+ * the RAM tier's page-aligned buffers (expert_cache.rs:55-253) allocated
+ * so H2D copies run asynchronously. */
+int mer_hip_host_alloc(size_t bytes, void **out);
+int mer_hip_host_free(void *p);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,5 +43,6 @@ from .expert import (
     take_device_status,
     validate_expert,
 )
+from .slots import SlotCache, pinned_expert_buffer
 
 __all__ = [n for n in dir() if not n.startswith("_")]

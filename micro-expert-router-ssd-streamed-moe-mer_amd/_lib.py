@@ -42,6 +42,11 @@ class MerGateOptions(ctypes.Structure):
     ]
 
 
+class MerSlotStats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in
+                ("hits", "misses", "prefetches", "evictions", "stale_retirements", "bytes_uploaded", "resident")]
+
+
 class MerErrorInfo(ctypes.Structure):
     _fields_ = [
         ("status", ctypes.c_int32),
@@ -102,6 +107,15 @@ SIGNATURES = {
     "mer_hip_route_linear_gate": (
         c_int, [c_void, c_size, c_size, c_void, c_size, c_size, ctypes.POINTER(MerGateOptions), c_void, c_void, c_void,
                 c_void]),
+    "mer_slot_cache_create": (c_int, [c_int, c_size, c_size, c_size, c_size, ctypes.POINTER(c_void)]),
+    "mer_slot_cache_destroy": (c_int, [c_void]),
+    "mer_slot_cache_table": (c_void, [c_void]),
+    "mer_slot_cache_prepare": (c_int, [c_void, c_void, c_void, c_void, c_size, c_void]),
+    "mer_slot_cache_prefetch": (c_int, [c_void, c_void, c_void, c_void, c_size, c_void]),
+    "mer_slot_cache_release": (c_int, [c_void, c_void]),
+    "mer_slot_cache_stats": (c_int, [c_void, ctypes.POINTER(MerSlotStats)]),
+    "mer_hip_host_alloc": (c_int, [c_size, ctypes.POINTER(c_void)]),
+    "mer_hip_host_free": (c_int, [c_void]),
     "mer_hip_fill_synthetic": (
         c_int, [c_int, c_u64, c_u64, c_u64, c_u64, c_float, c_float, c_void, c_void]),
 }

@@ -853,3 +853,11 @@ int mer_hip_fill_synthetic(int dtype, uint64_t seed, uint64_t expert_index, uint
 }
 
 }  // extern "C"
+
+namespace mer {
+
+int report_error(int status, const char *msg) { return fail(status, "%s", msg); }
+int report_hip_error(hipError_t e, int status, const char *what) { return hip_fail(e, status, what); }
+int check_initialised() { return require_init(); }
+
+}  // namespace mer

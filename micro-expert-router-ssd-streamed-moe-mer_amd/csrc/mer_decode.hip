@@ -56,13 +56,6 @@ __device__ __forceinline__ void st_dev(T *p, T v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// 16-byte device-scope load (buffer load with the SC1 cache policy).
-__device__ __forceinline__ uint4 ld_dev_b128(const void *base, uint32_t byte_off) {
-  const __amdgpu_buffer_rsrc_t r =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7fffffff, 0x00020000);
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16 /* SC1 */));
-}
-
 // Blob of expert instance `inst` of layer `la` (the same on every lane), or
 // null for a residency miss.  Read from the caller's routing arrays, which
 // were written before this launch, so ordinary loads see them.

@@ -166,4 +166,11 @@ hipError_t launch_fill(int fmt, uint64_t seed, uint64_t expert, uint64_t block_b
                        float lo, float hi, uint8_t *dst, hipStream_t st);
 hipError_t read_and_clear_device_status(uint32_t *out);
 
+// Error reporting shared by the C-ABI sources: record `msg` (and a HIP
+// error's text) as the calling thread's last error and return `status`.
+int report_error(int status, const char *msg);
+int report_hip_error(hipError_t e, int status, const char *what);
+// MER_OK once mer_hip_init has selected a device.
+int check_initialised();
+
 }  // namespace mer

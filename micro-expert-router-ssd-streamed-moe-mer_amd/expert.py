@@ -53,6 +53,14 @@ def _ptr(t: torch.Tensor, dtype: torch.dtype | None = None) -> int:
     return t.data_ptr()
 
 
+def _table(table) -> tuple[int, int]:
+    """(device pointer, length) of an expert table: an int64 device tensor of
+    blob pointers, or an object exposing table_ptr / table_len (SlotCache)."""
+    if isinstance(table, torch.Tensor):
+        return _ptr(table, torch.int64), table.numel()
+    return int(table.table_ptr), int(table.table_len)
+
+
 def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
@@ -160,7 +168,8 @@ def moe_forward(dtype: WeightDtype, d_model: int, d_ff: int, table: torch.Tensor
     """Routed experts + top-k weighted combine for a decode batch: the
     WeightedInto loop of moe_step_inner (engine.rs:5548-5639).
 
-    table      int64 [E] device pointers of resident expert blobs (0 = absent)
+    table      int64 [E] device pointers of resident expert blobs (0 = absent),
+               or a SlotCache (its device slot table)
     expert_ids int32 [n_tokens, top_k]
     weights    float32 [n_tokens, top_k]
     x          float32 [n_tokens, d_model]
@@ -172,8 +181,8 @@ def moe_forward(dtype: WeightDtype, d_model: int, d_ff: int, table: torch.Tensor
     if out is None:
         out = torch.empty_like(x)
     flags = (MOE_RESIDUAL if residual else 0) | (MOE_ACCUMULATE if accumulate else 0)
-    _call("mer_hip_moe_forward", int(dtype), d_model, d_ff, n_tokens, top_k, _ptr(table, torch.int64),
-          table.numel(), _ptr(expert_ids, torch.int32), _ptr(weights, torch.float32), _ptr(x, torch.float32),
+    _call("mer_hip_moe_forward", int(dtype), d_model, d_ff, n_tokens, top_k, *_table(table),
+          _ptr(expert_ids, torch.int32), _ptr(weights, torch.float32), _ptr(x, torch.float32),
           _ptr(out, torch.float32), flags, _stream())
     return out
 
@@ -203,7 +212,7 @@ def moe_forward_layers(dtype: WeightDtype, d_model: int, d_ff: int, layers, *, r
         if la["out"].shape != (n_tokens, d_model):
             raise ValueError("out must be [n_tokens, d_model]")
         x = la.get("x")
-        arr[i] = _lib.MerLayerArgs(_ptr(la["table"], torch.int64), la["table"].numel(), _ptr(la["ids"], torch.int32),
+        arr[i] = _lib.MerLayerArgs(*_table(la["table"]), _ptr(la["ids"], torch.int32),
                                    _ptr(la["weights"], torch.float32), 0 if x is None else _ptr(x, torch.float32),
                                    _ptr(la["out"], torch.float32))
     flags = ((MOE_RESIDUAL if residual else 0) | (MOE_ACCUMULATE if accumulate else 0) | (MOE_CHAIN if chain else 0)

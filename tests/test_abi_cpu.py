@@ -44,6 +44,13 @@ def test_uninitialised_calls_fail_cleanly(mer):
     rc = lib.mer_hip_expert_forward(4, None, 0, None, 0, 32, 32, None, 0, None)
     assert rc == mer._lib.Status.NOT_INITIALIZED
     assert b"mer_hip_init" in lib.mer_last_error()
+    h = ctypes.c_void_p()
+    assert lib.mer_slot_cache_create(4, 64, 64, 2, 4, ctypes.byref(h)) == mer._lib.Status.NOT_INITIALIZED
+    assert h.value is None
+    # null handles are rejected before any device work
+    assert lib.mer_slot_cache_prepare(None, None, None, None, 0, None) == mer._lib.Status.INVALID_LAYOUT
+    assert lib.mer_slot_cache_table(None) is None
+    assert lib.mer_slot_cache_destroy(None) == 0
 
 
 @pytest.mark.parametrize("dtype,dm,dff", [(4, 8, 8), (4, 10, 10), (5, 8, 8), (4, 4096, 14336), (4, 7168, 2048),
