@@ -183,6 +183,25 @@ int mer_hip_moe_forward(int dtype, size_t d_model, size_t d_ff,
                         const float *d_x, float *d_out, unsigned flags,
                         void *stream);
 
+/* Grouped path for multi-token batches (prefill): the same contract as
+ * mer_hip_moe_forward -- per token out = [x +] sum_i w_i y_i in slot order,
+ * zero-weight slots skipped, misses recorded in the device status -- but
+ * the routed (token, slot) pairs are grouped by expert on the device, so
+ * every expert's weights are read once for all of its tokens and the
+ * projections run as int8 MFMA contractions over token tiles of 16.  This
+ * is the batched counterpart of routed_expert_matmul_batch_q4
+ * (backend/mod.rs:4401-4418) and of the per-pair dispatch loop of
+ * forward_moe_resident_cpu (engine.rs:1761-1848) over a prefill batch.
+ * Requires d_model and d_ff to be multiples of 64, n_tokens * top_k <=
+ * 4096 and table_len <= 4096.  Inputs are held in 24-bit block fixed
+ * point (error <= 2^-24 of each 32-element block's maximum). */
+int mer_hip_moe_grouped(int dtype, size_t d_model, size_t d_ff,
+                        size_t n_tokens, size_t top_k,
+                        const void *const *d_expert_table, size_t table_len,
+                        const int32_t *d_expert_ids, const float *d_weights,
+                        const float *d_x, float *d_out, unsigned flags,
+                        void *stream);
+
 /* Per-layer arguments of mer_hip_moe_forward_layers (device pointers). */
 typedef struct mer_layer_args {
   const void *const *expert_table; /* [table_len] expert blob pointers    */

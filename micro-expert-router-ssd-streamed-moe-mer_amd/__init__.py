@@ -35,6 +35,7 @@ from .expert import (
     init,
     moe_forward,
     moe_forward_layers,
+    moe_grouped,
     q4_0_forward,
     q4_0_matvec,
     routed_expert_gpu_compatibility,

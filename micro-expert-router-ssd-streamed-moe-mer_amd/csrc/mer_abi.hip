@@ -528,6 +528,84 @@ int run_experts(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
   return timing_end(tl, st);
 }
 
+// Grouped multi-token path: group -> gate/up -> down -> combine.
+int run_grouped(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t top_k, const void *const *table,
+                uint32_t table_len, const int32_t *ids, const float *weights, const float *x, float *out,
+                unsigned flags, hipStream_t st) {
+  DeviceState &dev = g_dev[g_device];
+  GroupedParams p{};
+  p.table = table;
+  p.table_len = table_len;
+  p.ids = ids;
+  p.weights = weights;
+  p.x = x;
+  p.out = out;
+  p.flags = flags;
+  p.n_tok = n_tokens;
+  p.top_k = top_k;
+  p.n_pairs = n_tokens * top_k;
+  p.d_model = (uint32_t)dm;
+  p.d_ff = (uint32_t)dff;
+  p.xblocks = (uint32_t)(dm / 32);
+  p.hblocks = (uint32_t)(dff / 32);
+  p.proj_bytes = div_ceil(dm * dff, 32) * block_bytes(dtype);
+  p.status = dev.status;
+  // Token tiles hold <= 16 pairs of one expert: at most n_pairs / 16 full
+  // tiles plus one partial tile per distinct expert.
+  const uint32_t max_tiles = p.n_pairs / 16 + (p.n_pairs < table_len ? p.n_pairs : table_len);
+
+  auto up64 = [](size_t v) { return (v + 63) / 64 * 64; };  // floats; 256-byte aligned regions
+  const size_t n_hdr = 64;
+  const size_t n_plist = up64(p.n_pairs);
+  const size_t n_tiles = up64((size_t)max_tiles * sizeof(GroupTile) / 4);
+  const size_t n_xg = up64((size_t)n_tokens * p.xblocks * 24);
+  const size_t n_xs = up64((size_t)n_tokens * p.xblocks);
+  const size_t n_hg = up64((size_t)p.n_pairs * p.hblocks * 24);
+  const size_t n_hs = up64((size_t)p.n_pairs * p.hblocks);
+  const size_t n_pa = up64((size_t)p.n_pairs * dm);
+  const size_t total = n_hdr + n_plist + n_tiles + n_xg + n_xs + n_hg + n_hs + n_pa;
+  if (dev.scratch_floats < total && capturing(st))
+    return fail(MER_ERR_PHYSICAL_CAPACITY,
+                "scratch must grow, which cannot happen under graph capture: run the same call once before capturing");
+  float *cur = nullptr;
+  int rc = ensure_scratch(total, &cur);
+  if (rc) return rc;
+  p.n_tiles = reinterpret_cast<uint32_t *>(cur);
+  cur += n_hdr;
+  p.plist = reinterpret_cast<uint32_t *>(cur);
+  cur += n_plist;
+  p.tiles = reinterpret_cast<GroupTile *>(cur);
+  cur += n_tiles;
+  p.xg = reinterpret_cast<uint32_t *>(cur);
+  cur += n_xg;
+  p.xs = cur;
+  cur += n_xs;
+  p.hg = reinterpret_cast<uint32_t *>(cur);
+  cur += n_hg;
+  p.hs = cur;
+  cur += n_hs;
+  p.partial = cur;
+
+  const int fmt = fmt_of(dtype);
+  TimedLaunch *tl = nullptr;
+  int trc;
+  hipError_t e;
+  if ((trc = timing_begin(STAGE_PREP, st, &tl))) return trc;
+  if ((e = launch_grouped_prep(p, st)) != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "grouping launch");
+  if ((trc = timing_end(tl, st))) return trc;
+  if ((trc = timing_begin(STAGE_GATE_UP, st, &tl))) return trc;
+  if ((e = launch_grouped_proj(fmt, true, p, max_tiles, st)) != hipSuccess)
+    return hip_fail(e, MER_ERR_SUBMISSION, "grouped gate/up launch");
+  if ((trc = timing_end(tl, st))) return trc;
+  if ((trc = timing_begin(STAGE_DOWN, st, &tl))) return trc;
+  if ((e = launch_grouped_proj(fmt, false, p, max_tiles, st)) != hipSuccess)
+    return hip_fail(e, MER_ERR_SUBMISSION, "grouped down launch");
+  if ((trc = timing_end(tl, st))) return trc;
+  if ((trc = timing_begin(STAGE_COMBINE, st, &tl))) return trc;
+  if ((e = launch_grouped_combine(p, st)) != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "grouped combine launch");
+  return timing_end(tl, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -757,6 +835,33 @@ int mer_hip_moe_forward(int dtype, size_t d_model, size_t d_ff, size_t n_tokens,
     return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
   return run_experts(dtype, d_model, d_ff, (uint32_t)n_tokens, (uint32_t)top_k, d_expert_table, (uint32_t)table_len,
                      d_expert_ids, nullptr, d_weights, d_x, d_out, flags, (hipStream_t)stream, false);
+}
+
+int mer_hip_moe_grouped(int dtype, size_t d_model, size_t d_ff, size_t n_tokens, size_t top_k,
+                        const void *const *d_expert_table, size_t table_len, const int32_t *d_expert_ids,
+                        const float *d_weights, const float *d_x, float *d_out, unsigned flags, void *stream) {
+  int rc = require_init();
+  if (rc) return rc;
+  if (dtype != MER_DTYPE_Q4_0 && dtype != MER_DTYPE_Q8_0)
+    return fail(MER_ERR_UNSUPPORTED_DTYPE, "unsupported expert dtype %d", dtype);
+  rc = mer_routed_expert_gpu_compatibility(dtype, d_model, d_ff);
+  if (rc) return rc;
+  if (flags & ~3u) return fail(MER_ERR_INVALID_LAYOUT, "unknown flags 0x%x", flags);
+  if ((flags & 3u) == 3u) return fail(MER_ERR_INVALID_LAYOUT, "RESIDUAL and ACCUMULATE are exclusive");
+  if (d_model == 0 || d_ff == 0 || d_model % 64 || d_ff % 64)
+    return fail(MER_ERR_INVALID_LAYOUT, "the grouped path needs d_model and d_ff to be non-zero multiples of 64, got %zu, %zu",
+                d_model, d_ff);
+  if (n_tokens == 0 || top_k == 0) return MER_OK;
+  if (n_tokens * top_k > kMaxGroupedPairs)
+    return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "the grouped path takes at most %u routed pairs, got %zu",
+                kMaxGroupedPairs, n_tokens * top_k);
+  if (table_len == 0 || table_len > kMaxGroupedExperts)
+    return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "the grouped path takes expert tables of 1..%u entries, got %zu",
+                kMaxGroupedExperts, table_len);
+  if (!d_expert_table || !d_expert_ids || !d_weights || !d_x || !d_out)
+    return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
+  return run_grouped(dtype, d_model, d_ff, (uint32_t)n_tokens, (uint32_t)top_k, d_expert_table, (uint32_t)table_len,
+                     d_expert_ids, d_weights, d_x, d_out, flags, (hipStream_t)stream);
 }
 
 int mer_hip_moe_forward_layers(int dtype, size_t d_model, size_t d_ff, size_t n_layers, size_t n_tokens,

@@ -1,0 +1,506 @@
+// mer_grouped.hip -- grouped per-expert path for multi-token batches (gfx950).
+//
+// A prefill-sized batch routes many tokens to the same expert, so each
+// expert's weights can be read once for all of its tokens.  That turns
+// the per-expert work into a real dense contraction: [rows x K] weights by
+// [K x tokens], run on int8 MFMA (v_mfma_i32_16x16x32_i8, K = 32 = one
+// GGUF block).  Reference semantics are those of the decode path: every
+// routed (token, slot) pair computes y = W_down (silu(W_gate x) * (W_up x))
+// (inference.rs:3291-3306 / :3636-3746) and the token's output is
+// [x +] sum_i w_i y_i in slot order (combine_outputs_into,
+// inference.rs:4472-4491; the WeightedInto loop, engine.rs:5548-5639).
+//
+// Launches, all on the caller's stream:
+//   group_kernel   block 0 groups the routed pairs by expert (counting
+//                  sort) and emits token tiles of <= 16 pairs per expert;
+//                  the other blocks quantise x into 16-bit digit pairs
+//   proj_kernel<FUSED>  one workgroup per (token tile, 32 rows of d_ff):
+//                  gate and up rows for the tile's tokens, SiLU * up, h
+//                  quantised per 32-element block
+//   proj_kernel<!FUSED> one workgroup per (token tile, 64 rows of d_model):
+//                  down rows -> w_i * y_i per pair
+//   combine_kernel out[t] = [x +] sum over slots in slot order
+//
+// Numerics.  The weights are int8 (Q8_0 q, or Q4_0 q-8) with one f16
+// scale per 32-weight block.  Each 32-element block b of an input vector
+// (x, or h for the down projection) is held as s_b * v with
+// s_b = max|x_b| / 8355711 and v = round(x / s_b), split into three signed
+// base-256 digits v = v0 + 256 v1 + 65536 v2 (the bytes of v + 0x808080
+// with their top bits flipped).  Per block, MFMA gives the exact int32
+// sums Pk = sum q*vk (|Pk| < 2^19); P1 + 256 P2 is exact in int32, and the
+// block contributes (256 (P1 + 256 P2) + P0) * d_w * s_b, formed in f32,
+// to an f32 accumulator.  The representation error of v is at most 2^-24
+// of the block's largest |x| (an f32 rounding of that element); non-finite
+// inputs give a NaN scale, so NaN propagates.
+//
+// Operand layout of v_mfma_i32_16x16x32_i8: lane l holds 8 int8 of A row
+// (l % 16) and of B column (l % 16), covering the same 8 of the block's 32
+// k-indices (chosen by l / 16) in A and B; output lane l holds rows
+// 4 (l / 16) + i, i = 0..3, of column l % 16.  Weights are staged through
+// LDS as [row][block][32 int8] (rows padded to spread banks) plus f32
+// scales [block][row]; the input digits are stored per (vector, block) as
+// 4 groups x {8 bytes v0, 8 bytes v1, 8 bytes v2}, so a lane reads the B
+// operands of its k-group from one 24-byte record.
+#include "mer_internal.hpp"
+
+namespace mer {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kGTok = 16;           // pairs per token tile (MFMA N)
+constexpr uint32_t kGRows = 64;          // weight rows staged per workgroup
+constexpr uint32_t kGStageBlocks = 16;   // K blocks per LDS stage
+constexpr uint32_t kGRowStride = kGStageBlocks * 32 + 16;  // LDS bytes per staged row
+constexpr float kGIntMax = 8355711.0f;   // |v| bound (0x7f7f7f): v + 0x808080 stays in 24 bits
+constexpr uint32_t kGRec = 6;            // dwords per (vector, block, k-group) digit record
+constexpr uint32_t kNoChunkG = 0x80000000u;
+
+__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
+
+__device__ __forceinline__ void record_status(uint32_t *status, uint32_t code) { atomicCAS(status, 0u, code); }
+
+__device__ __forceinline__ bool pair_valid(const GroupedParams &p, uint32_t pair, const uint8_t **blob) {
+  if (p.weights && p.weights[pair] == 0.0f) return false;  // skipped by the combine (engine.rs:5575-5580)
+  const int32_t id = p.ids[pair];
+  if (id < 0 || (uint32_t)id >= p.table_len) return false;
+  const uint8_t *b = reinterpret_cast<const uint8_t *>(p.table[id]);
+  if (blob) *blob = b;
+  return b != nullptr;
+}
+
+// Quantise 8 elements (one MFMA k-group) of a block whose 4 groups sit in
+// 4 adjacent lanes (lane & 3 = group): block max by shuffles, then the three
+// digit planes as one 24-byte record {v0[8], v1[8], v2[8]}.
+// Only lanes with `store` write; the group's first lane writes the scale.
+__device__ __forceinline__ void quant_group(const float (&v)[8], uint32_t *dst, float *scale, bool lead, bool store) {
+  float amax = 0.f;
+  int finite = 1;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
+    finite &= __builtin_isfinite(v[i]) ? 1 : 0;
+  }
+#pragma unroll
+  for (int off = 1; off < 4; off <<= 1) {
+    amax = __builtin_fmaxf(amax, __shfl_xor(amax, off, 64));
+    finite &= __shfl_xor(finite, off, 64);
+  }
+  float s, inv;
+  if (!finite) {
+    s = __builtin_nanf("");
+    inv = 0.f;
+  } else if (amax == 0.f) {
+    s = 0.f;
+    inv = 0.f;
+  } else {
+    s = amax / kGIntMax;
+    inv = kGIntMax / amax;
+  }
+  uint32_t d[kGRec] = {0u, 0u, 0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float q = __builtin_rintf(v[i] * inv);
+    q = __builtin_fminf(__builtin_fmaxf(q, -kGIntMax), kGIntMax);
+    const uint32_t u = ((uint32_t)((int32_t)q + 0x808080)) ^ 0x808080u;  // three balanced digits
+#pragma unroll
+    for (int k = 0; k < 3; ++k) d[2 * k + (i >> 2)] |= ((u >> (8 * k)) & 0xffu) << (8 * (i & 3));
+  }
+  if (!store) return;
+  uint2 *o = reinterpret_cast<uint2 *>(dst);
+  o[0] = make_uint2(d[0], d[1]);
+  o[1] = make_uint2(d[2], d[3]);
+  o[2] = make_uint2(d[4], d[5]);
+  if (lead) *scale = s;
+}
+
+// Block 0: group the routed pairs by expert.  Other blocks: quantise x.
+__global__ __launch_bounds__(1024) void group_kernel(GroupedParams p) {
+  if (blockIdx.x > 0) {
+    const uint32_t g = (blockIdx.x - 1) * blockDim.x + threadIdx.x;  // (token, block, group)
+    const uint32_t total = p.n_tok * p.xblocks * 4;
+    // whole quads stay together for the shuffles; quads past the end idle
+    const bool valid = g < total;
+    const uint32_t tb = g / 4, m = g % 4;
+    float v[8];
+    if (valid) {
+      const float4 a = *reinterpret_cast<const float4 *>(p.x + (size_t)tb * 32 + 8 * m);
+      const float4 b = *reinterpret_cast<const float4 *>(p.x + (size_t)tb * 32 + 8 * m + 4);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = 0.f;
+    }
+    quant_group(v, p.xg + ((size_t)tb * 4 + m) * kGRec, p.xs + tb, m == 0, valid);
+    return;
+  }
+
+  extern __shared__ uint32_t sh[];
+  uint32_t *cnt = sh;                   // [table_len] pairs per expert, then offsets
+  uint32_t *tcnt = sh + p.table_len;    // [table_len] tiles per expert, then offsets
+  uint32_t *pos = tcnt + p.table_len;   // [n_pairs] rank of a pair within its expert
+  __shared__ uint32_t part[1024 * 2];
+  const uint32_t tid = threadIdx.x, nth = blockDim.x;
+  for (uint32_t e = tid; e < p.table_len; e += nth) cnt[e] = 0u;
+  __syncthreads();
+  for (uint32_t q = tid; q < p.n_pairs; q += nth) {
+    const uint8_t *blob = nullptr;
+    if (pair_valid(p, q, &blob)) {
+      pos[q] = atomicAdd(&cnt[p.ids[q]], 1u);
+    } else {
+      pos[q] = 0xffffffffu;
+      if (!(p.weights && p.weights[q] == 0.0f)) record_status(p.status, 16u /* MER_ERR_RESIDENCY_MISS */);
+    }
+  }
+  __syncthreads();
+  // exclusive scans of pairs and tiles per expert: each thread owns a run
+  // of consecutive experts
+  const uint32_t per = (p.table_len + nth - 1) / nth;
+  const uint32_t e0 = tid * per, e1 = min(p.table_len, e0 + per);
+  uint32_t sp = 0, st = 0;
+  for (uint32_t e = e0; e < e1; ++e) {
+    const uint32_t c = cnt[e];
+    sp += c;
+    st += (c + kGTok - 1) / kGTok;
+  }
+  part[tid] = sp;
+  part[nth + tid] = st;
+  __syncthreads();
+  for (uint32_t off = 1; off < nth; off <<= 1) {  // Hillis-Steele inclusive scan
+    uint32_t a = 0, b = 0;
+    if (tid >= off) {
+      a = part[tid - off];
+      b = part[nth + tid - off];
+    }
+    __syncthreads();
+    part[tid] += a;
+    part[nth + tid] += b;
+    __syncthreads();
+  }
+  uint32_t op = part[tid] - sp, ot = part[nth + tid] - st;
+  for (uint32_t e = e0; e < e1; ++e) {
+    const uint32_t c = cnt[e];
+    const uint32_t nt = (c + kGTok - 1) / kGTok;
+    cnt[e] = op;
+    tcnt[e] = ot;
+    for (uint32_t j = 0; j < nt; ++j) {
+      GroupTile t;
+      t.blob = reinterpret_cast<const uint8_t *>(p.table[e]);
+      t.start = op + j * kGTok;
+      t.count = min(kGTok, c - j * kGTok);
+      p.tiles[ot + j] = t;
+    }
+    op += c;
+    ot += nt;
+  }
+  if (tid == nth - 1) *p.n_tiles = part[nth + tid];
+  __syncthreads();
+  for (uint32_t q = tid; q < p.n_pairs; q += nth)
+    if (pos[q] != 0xffffffffu) p.plist[cnt[p.ids[q]] + pos[q]] = q;
+}
+
+// Stage one 64-row x 16-block slab of weights into LDS: 512 two-block
+// chunks, two per thread, loaded with raw buffer loads (a chunk past the
+// row's end reads zeros) and stored as int8 rows plus f32 scales.
+template <int FMT>
+struct Stager {
+  using T = FmtTraits<FMT>;
+  static constexpr int kDw = T::kChunkDwords;
+  __amdgpu_buffer_rsrc_t rsrc[2];
+  uint32_t voff[2];      // byte offset of this thread's chunk c (stage 0), or kNoChunkG
+  uint32_t srow[2], schunk[2];
+  uint32_t w[2][kDw];
+
+  // fused: slab rows 0..31 come from base0 (gate), rows 32..63 from base1
+  // (up), both starting at row 0; otherwise all 64 rows from base0.
+  __device__ __forceinline__ void init(const uint8_t *base0, const uint8_t *base1, uint32_t row_bytes, bool fused) {
+    rsrc[0] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base0), 0, 0x7fffffff, 0x00020000);
+    rsrc[1] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base1), 0, 0x7fffffff, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t c = threadIdx.x + 256u * i;  // chunk of the slab: row c / 8, chunk c % 8
+      srow[i] = c / 8;
+      schunk[i] = c % 8;
+      const uint32_t r = fused ? srow[i] % 32 : srow[i];
+      voff[i] = r * row_bytes + schunk[i] * (uint32_t)T::kChunkBytes;
+    }
+  }
+
+  // Issue the loads of stage s (chunks s*8 .. s*8+7 of each row).
+  __device__ __forceinline__ void load(uint32_t s, uint32_t row_chunks, bool fused) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int which = fused && srow[i] >= 32 ? 1 : 0;
+      const bool ok = s * 8 + schunk[i] < row_chunks;
+      const uint32_t off = ok ? voff[i] + s * 8u * (uint32_t)T::kChunkBytes : kNoChunkG;
+#pragma unroll
+      for (int v = 0; v < kDw / 4; ++v) {
+        const uint4 q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc[which], off + 16 * v, 0, 0));
+        w[i][4 * v] = q.x;
+        w[i][4 * v + 1] = q.y;
+        w[i][4 * v + 2] = q.z;
+        w[i][4 * v + 3] = q.w;
+      }
+      w[i][kDw - 1] = __builtin_amdgcn_raw_buffer_load_b32(rsrc[which], off + 16 * (kDw / 4), 0, 0);
+    }
+  }
+
+  // Write the loaded chunks to LDS: q as int8 [row][block][32], scales
+  // as f32 [block][row].
+  __device__ __forceinline__ void store(uint8_t *lq, float *ld) const {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      uint32_t q0[8], q1[8];
+      float d0, d1;
+      if constexpr (FMT == FMT_Q4_0) {
+        // block 0: d = w0[15:0], qs = bytes 2..17; block 1: d = w4[31:16], qs = w5..w8
+        const uint32_t a[4] = {realign16(w[i][0], w[i][1]), realign16(w[i][1], w[i][2]), realign16(w[i][2], w[i][3]),
+                               realign16(w[i][3], w[i][4])};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          // element j = low nibble of qs[j], j + 16 = high nibble; int8 q - 8
+          q0[m] = ((a[m] & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
+          q0[4 + m] = (((a[m] >> 4) & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
+          const uint32_t b = w[i][5 + m];
+          q1[m] = ((b & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
+          q1[4 + m] = (((b >> 4) & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
+        }
+        d0 = f16_bits_to_f32(w[i][0] & 0xffffu);
+        d1 = f16_bits_to_f32(w[i][4] >> 16);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          q0[k] = realign16(w[i][k], w[i][k + 1]);
+          q1[k] = w[i][9 + k];
+        }
+        d0 = f16_bits_to_f32(w[i][0] & 0xffffu);
+        d1 = f16_bits_to_f32(w[i][8] >> 16);
+      }
+      const uint32_t b0 = 2 * schunk[i];
+      uint4 *dst = reinterpret_cast<uint4 *>(lq + srow[i] * kGRowStride + b0 * 32);
+      dst[0] = make_uint4(q0[0], q0[1], q0[2], q0[3]);
+      dst[1] = make_uint4(q0[4], q0[5], q0[6], q0[7]);
+      dst[2] = make_uint4(q1[0], q1[1], q1[2], q1[3]);
+      dst[3] = make_uint4(q1[4], q1[5], q1[6], q1[7]);
+      ld[b0 * kGRows + srow[i]] = d0;
+      ld[(b0 + 1) * kGRows + srow[i]] = d1;
+    }
+  }
+};
+
+// One workgroup (4 waves) per (token tile, 64 staged rows).  FUSED: rows
+// 0..31 are gate rows r0.., rows 32..63 the same up rows; the epilogue
+// writes h = silu(g) * u for 32 rows = one block per pair.  Otherwise 64
+// down rows; the epilogue writes w_i * y_i per pair.
+template <int FMT, bool FUSED>
+__global__ __launch_bounds__(256) void gproj_kernel(GroupedParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lq[kGRows * kGRowStride];
+  __shared__ __attribute__((aligned(16))) float ld[kGStageBlocks * kGRows];
+  __shared__ uint32_t s_pair[kGTok];
+
+  const uint32_t row_tiles = FUSED ? p.d_ff / 32 : p.d_model / kGRows;
+  const uint32_t tile = blockIdx.x / row_tiles;
+  const uint32_t rt = blockIdx.x % row_tiles;
+  if (tile >= *p.n_tiles) return;  // uniform over the workgroup
+  const GroupTile gt = p.tiles[tile];
+  const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / 64u;
+  if (tid < kGTok) s_pair[tid] = tid < gt.count ? p.plist[gt.start + tid] : 0xffffffffu;
+
+  const uint32_t kblocks = FUSED ? p.xblocks : p.hblocks;  // K / 32
+  const uint32_t row_chunks = kblocks / 2;
+  const uint32_t row_bytes = kblocks * (uint32_t)FmtTraits<FMT>::kBlockBytes;
+  Stager<FMT> sg;
+  if constexpr (FUSED) {
+    const uint8_t *g = gt.blob + (size_t)rt * 32 * row_bytes;
+    sg.init(g, g + p.proj_bytes, row_bytes, true);
+  } else {
+    const uint8_t *d = gt.blob + 2 * p.proj_bytes + (size_t)rt * kGRows * row_bytes;
+    sg.init(d, d, row_bytes, false);
+  }
+  sg.load(0, row_chunks, FUSED);
+  __syncthreads();  // s_pair
+
+  // B operands: the lane's column is pair s_pair[lane % 16]; its k-group is lane / 16
+  const uint32_t col = lane % 16, kg = lane / 16;
+  const uint32_t pair = s_pair[col];
+  const bool col_ok = pair != 0xffffffffu;
+  const uint2 *vdig;  // the lane's record of block 0; block b is 4 * kGRec / 2 uint2 further
+  const float *vsc;
+  if constexpr (FUSED) {
+    const uint32_t t = col_ok ? pair / p.top_k : 0;
+    vdig = reinterpret_cast<const uint2 *>(p.xg + ((size_t)t * p.xblocks * 4 + kg) * kGRec);
+    vsc = p.xs + (size_t)t * p.xblocks;
+  } else {
+    const uint32_t pr = col_ok ? pair : 0;
+    vdig = reinterpret_cast<const uint2 *>(p.hg + ((size_t)pr * p.hblocks * 4 + kg) * kGRec);
+    vsc = p.hs + (size_t)pr * p.hblocks;
+  }
+
+  float acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[a][i] = 0.f;
+
+  const uint32_t n_stages = (kblocks + kGStageBlocks - 1) / kGStageBlocks;
+  for (uint32_t s = 0; s < n_stages; ++s) {
+    sg.store(lq, ld);
+    __syncthreads();
+    if (s + 1 < n_stages) sg.load(s + 1, row_chunks, FUSED);
+    const uint32_t nb = min(kGStageBlocks, kblocks - s * kGStageBlocks);
+    // this wave's blocks of the stage: wave, wave + 4, wave + 8, wave + 12
+    uint2 bv[4][3];
+    float bs[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t b = wave + 4 * j;
+      const bool ok = col_ok && b < nb;
+      const uint32_t gb = s * kGStageBlocks + b;
+#pragma unroll
+      for (int k = 0; k < 3; ++k) bv[j][k] = ok ? vdig[(size_t)gb * 2 * kGRec + k] : make_uint2(0, 0);
+      bs[j] = ok ? vsc[gb] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t b = wave + 4 * j;
+      if (b >= nb) break;  // uniform
+      long bk[3];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) bk[k] = (long)(((uint64_t)bv[j][k].y << 32) | bv[j][k].x);
+      v4i p0[4], p1[4], p2[4];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const long av = *reinterpret_cast<const long *>(lq + (a * 16 + col) * kGRowStride + b * 32 + kg * 8);
+        const v4i z = {0, 0, 0, 0};
+        p0[a] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[0], z, 0, 0, 0);
+        p1[a] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[1], z, 0, 0, 0);
+        p2[a] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[2], z, 0, 0, 0);
+      }
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const float4 d = *reinterpret_cast<const float4 *>(&ld[b * kGRows + a * 16 + kg * 4]);
+        const float dd[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float hi = (float)(p1[a][i] + (p2[a][i] << 8));
+          const float v = __builtin_fmaf(hi, 256.0f, (float)p0[a][i]);
+          acc[a][i] = __builtin_fmaf(v, dd[i] * bs[j], acc[a][i]);
+        }
+      }
+    }
+    __syncthreads();  // LDS slab consumed before the next store
+  }
+
+  // sum the four waves' partials (in the slab's LDS, free now); wave w
+  // then owns row tile w
+  typedef float RedT[4][64][4];  // [row tile][lane][i]
+  RedT *red = reinterpret_cast<RedT *>(lq);
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+    *reinterpret_cast<float4 *>(&red[wave][a][lane][0]) = make_float4(acc[a][0], acc[a][1], acc[a][2], acc[a][3]);
+  __syncthreads();
+  float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {  // fixed order
+    const float4 v = *reinterpret_cast<const float4 *>(&red[w][wave][lane][0]);
+    sum.x += v.x;
+    sum.y += v.y;
+    sum.z += v.z;
+    sum.w += v.w;
+  }
+  // lane holds rows wave*16 + 4*kg + i of column col
+
+  if constexpr (FUSED) {
+    __syncthreads();
+    float *fin = reinterpret_cast<float *>(lq);  // [64 rows][16 cols]
+    const uint32_t r = wave * 16 + 4 * kg;
+    fin[(r + 0) * kGTok + col] = sum.x;
+    fin[(r + 1) * kGTok + col] = sum.y;
+    fin[(r + 2) * kGTok + col] = sum.z;
+    fin[(r + 3) * kGTok + col] = sum.w;
+    __syncthreads();
+    if (tid < 64) {
+      // pair column c = tid / 4, k-group m = tid % 4: h rows 8m .. 8m+7
+      const uint32_t c = tid / 4, m = tid % 4;
+      float h[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float g = fin[(8 * m + i) * kGTok + c];
+        const float u = fin[(32 + 8 * m + i) * kGTok + c];
+        h[i] = silu_mul(g, u);
+      }
+      const uint32_t pr = s_pair[c];
+      const bool ok = pr != 0xffffffffu;
+      const size_t hb = (size_t)(ok ? pr : 0) * p.hblocks + rt;
+      quant_group(h, p.hg + (hb * 4 + m) * kGRec, p.hs + hb, m == 0, ok);
+    }
+  } else {
+    if (col_ok) {
+      const float w = p.weights ? p.weights[pair] : 1.0f;
+      const uint32_t r = rt * kGRows + wave * 16 + 4 * kg;
+      *reinterpret_cast<float4 *>(p.partial + (size_t)pair * p.d_model + r) =
+          make_float4(w * sum.x, w * sum.y, w * sum.z, w * sum.w);
+    }
+  }
+}
+
+// out[t] = [x +] sum over the token's valid slots, in slot order, of the
+// pair partials (w_i y_i).  One thread per 4 output elements.
+__global__ __launch_bounds__(256) void gcombine_kernel(GroupedParams p) {
+  const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t per_tok = p.d_model / 4;
+  if (q >= p.n_tok * per_tok) return;
+  const uint32_t t = q / per_tok, c = (q % per_tok) * 4;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (uint32_t k = 0; k < p.top_k; ++k) {
+    const uint32_t pr = t * p.top_k + k;
+    if (!pair_valid(p, pr, nullptr)) continue;
+    const float4 v = *reinterpret_cast<const float4 *>(p.partial + (size_t)pr * p.d_model + c);
+    acc.x += v.x;
+    acc.y += v.y;
+    acc.z += v.z;
+    acc.w += v.w;
+  }
+  float4 *o = reinterpret_cast<float4 *>(p.out + (size_t)t * p.d_model + c);
+  if (p.flags & (kFlagResidual | kFlagAccumulate)) {
+    const float4 base = (p.flags & kFlagResidual) ? *reinterpret_cast<const float4 *>(p.x + (size_t)t * p.d_model + c)
+                                                  : *o;
+    acc = make_float4(base.x + acc.x, base.y + acc.y, base.z + acc.z, base.w + acc.w);
+  }
+  *o = acc;
+}
+
+}  // namespace
+
+size_t grouped_group_lds_bytes(uint32_t table_len, uint32_t n_pairs) {
+  return (size_t)(2 * table_len + n_pairs) * 4;
+}
+
+hipError_t launch_grouped_prep(const GroupedParams &p, hipStream_t st) {
+  const uint32_t quads = p.n_tok * p.xblocks * 4;
+  const uint32_t gblocks = 1 + (quads + 1023) / 1024;
+  hipLaunchKernelGGL(group_kernel, dim3(gblocks), dim3(1024), grouped_group_lds_bytes(p.table_len, p.n_pairs), st, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_grouped_proj(int fmt, bool fused, const GroupedParams &p, uint32_t max_tiles, hipStream_t st) {
+  const uint32_t grid = max_tiles * (fused ? p.d_ff / 32 : p.d_model / kGRows);
+  if (fmt == FMT_Q4_0) {
+    if (fused) hipLaunchKernelGGL((gproj_kernel<FMT_Q4_0, true>), dim3(grid), dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((gproj_kernel<FMT_Q4_0, false>), dim3(grid), dim3(256), 0, st, p);
+  } else {
+    if (fused) hipLaunchKernelGGL((gproj_kernel<FMT_Q8_0, true>), dim3(grid), dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((gproj_kernel<FMT_Q8_0, false>), dim3(grid), dim3(256), 0, st, p);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_grouped_combine(const GroupedParams &p, hipStream_t st) {
+  const uint32_t cq = p.n_tok * (p.d_model / 4);
+  hipLaunchKernelGGL(gcombine_kernel, dim3((cq + 255) / 256), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+}  // namespace mer

@@ -130,6 +130,44 @@ struct DecodeParams {
   uint64_t trace_cap;
 };
 
+// ---- grouped multi-token path (mer_grouped.hip) --------------------------
+constexpr uint32_t kMaxGroupedExperts = 4096;  // table entries the grouping kernel counts in LDS
+constexpr uint32_t kMaxGroupedPairs = 4096;    // routed (token, slot) pairs per call
+
+struct GroupTile {
+  const uint8_t *blob;  // the expert's blob
+  uint32_t start;       // first pair of the tile in plist
+  uint32_t count;       // pairs in the tile (1..16)
+};
+
+struct GroupedParams {
+  const void *const *table;
+  uint32_t table_len;
+  const int32_t *ids;        // [n_tok * top_k]
+  const float *weights;      // [n_tok * top_k] or null (weight 1, no skip)
+  const float *x;            // [n_tok][d_model]
+  float *out;                // [n_tok][d_model]
+  uint32_t flags;
+  uint32_t n_tok, top_k, n_pairs;
+  uint32_t d_model, d_ff, xblocks, hblocks;
+  size_t proj_bytes;
+  // scratch
+  uint32_t *xg;              // x digits [n_tok][xblocks][4 k-groups][6 dwords]
+  float *xs;                 // x block scales [n_tok][xblocks]
+  uint32_t *hg;              // h digits [n_pairs][hblocks][4][6 dwords]
+  float *hs;                 // h block scales [n_pairs][hblocks]
+  float *partial;            // w_i y_i [n_pairs][d_model]
+  uint32_t *plist;           // pairs grouped by expert [n_pairs]
+  GroupTile *tiles;          // [max tiles]
+  uint32_t *n_tiles;         // tiles emitted by the grouping kernel
+  uint32_t *status;
+};
+
+size_t grouped_group_lds_bytes(uint32_t table_len, uint32_t n_pairs);
+hipError_t launch_grouped_prep(const GroupedParams &p, hipStream_t st);
+hipError_t launch_grouped_proj(int fmt, bool fused, const GroupedParams &p, uint32_t max_tiles, hipStream_t st);
+hipError_t launch_grouped_combine(const GroupedParams &p, hipStream_t st);
+
 // ---- LinearGate router (mer_router.hip) -----------------------------------
 constexpr uint32_t kMaxRouterExperts = 1024;
 constexpr uint32_t kMaxRouterTopK = 64;

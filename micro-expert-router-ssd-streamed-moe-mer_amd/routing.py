@@ -150,3 +150,21 @@ def route_linear_gate_gpu(gate, x, top_k: int, *, sigmoid: bool = False, normali
     if rc:
         errors.raise_for_status(rc)
     return (ids, weights, logits) if return_logits else (ids, weights)
+
+
+def zipf_skewed_routes(n_tokens: int, n_experts: int, top_k: int, zipf_s: float, seed: int):
+    """Routing of the batched grouped-expert workload: per token, logits
+    N(0,1) + ln p_zipf(rank(e); s), where rank is a seeded permutation of the
+    experts and p_zipf(r) is proportional to 1 / (r + 1)^s; then the default
+    gate's softmax, top-k and renormalisation (route_scores, gating.rs:395-476).
+    Returns ids int32 [n_tokens, top_k] and weights f32 [n_tokens, top_k]."""
+    rng = np.random.default_rng(seed)
+    rank = rng.permutation(n_experts)
+    p = 1.0 / np.power(np.arange(1, n_experts + 1, dtype=np.float64), zipf_s)
+    bias = np.log(p / p.sum())[rank].astype(np.float32)
+    ids = np.zeros((n_tokens, top_k), np.int32)
+    w = np.zeros((n_tokens, top_k), np.float32)
+    for t in range(n_tokens):
+        logits = rng.standard_normal(n_experts).astype(np.float32) + bias
+        ids[t], w[t] = route_scores(logits, top_k)
+    return ids, w

@@ -43,6 +43,7 @@ def assert_ffn_close(got, ref, label):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     assert got.shape == ref.shape, label
+    got, ref = got.ravel(), ref.ravel()
     assert np.isfinite(got).all(), label
     err = np.abs(got - ref)
     scale = max(1.0, float(np.abs(ref).max()))
