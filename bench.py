@@ -18,6 +18,11 @@ generator (nibbles uniform, d = f16(U(0.005, 0.02))).
   (d_model 2048, d_ff 768; 30.8 GB resident), top-8 from a per-layer
   LinearGate [128 x 2048] ~ N(0, 0.02) applied to a fresh N(0,1) hidden
   state per step and layer (routed on the host).
+--config 3: the batched grouped-expert case, 64 tokens x 128 Qwen3-shaped
+  Q8_0 experts, top-8 from N(0,1) logits plus a Zipf(1.1) popularity skew
+  (routing.zipf_skewed_routes), one mer_hip_moe_grouped call per step.  Steps
+  cycle over 8 copies of the 128-expert layer (5.1 GB) with fresh routing and
+  inputs, so no step finds its experts in the memory-side cache.
 
 Prints one JSON line.  The CPU baseline leg times the C oracle's
 restatement of the reference's CPU path on a bounded sample of the same
@@ -53,6 +58,10 @@ CONFIGS = {
             top_k=2, scale=(0.005, 0.02), metric=METRIC, unit="tokens/s"),
     2: dict(workload="qwen3-30b-a3b-moe-decode-q8_0-top8", dtype=Q8, d_model=2048, d_ff=768, layers=48, experts=128,
             top_k=8, scale=(0.002, 0.01), metric="expert-FFN tokens/s + achieved HBM GB/s, Qwen3-30B-A3B-shape Q8_0 top-8",
+            unit="tokens/s"),
+    3: dict(workload="qwen3-moe-grouped-64tok-q8_0-top8-zipf1.1", dtype=Q8, d_model=2048, d_ff=768, layers=8,
+            experts=128, top_k=8, tokens=64, scale=(0.002, 0.01),
+            metric="expert-FFN tokens/s + achieved HBM GB/s, 64-token Qwen3-shape Q8_0 top-8 grouped batch",
             unit="tokens/s"),
 }
 
@@ -193,6 +202,40 @@ def main() -> int:
         x_ref = xs[0]
         experts_per_step = 1
         routing_desc = "none (one expert per step)"
+    elif args.config == 3:
+        T = cfg["tokens"]
+        table = torch.tensor([[base + (l * E + e) * ebytes for e in range(E)] for l in range(L)],
+                             dtype=torch.int64, device=dev)
+        ids = np.zeros((total_steps, T, K), np.int32)
+        wts = np.zeros((total_steps, T, K), np.float32)
+        for s in range(total_steps):
+            ids[s], wts[s] = routing.zipf_skewed_routes(T, E, K, 1.1, seed=args.seed + 2 + s)
+        xs = rng_x.standard_normal((total_steps, T, dm)).astype(np.float32)
+        ids_d = torch.from_numpy(ids).to(dev)
+        wts_d = torch.from_numpy(wts).to(dev)
+        xs_d = torch.from_numpy(xs).to(dev)
+        out = torch.zeros((T, dm), dtype=torch.float32, device=dev)
+        distinct = np.array([len(np.unique(ids[s])) for s in range(total_steps)])
+        step_bytes_list = distinct * ebytes + 2 * T * dm * 4  # distinct experts' weights + x in + out
+        fn = lib.mer_hip_moe_grouped
+        all_args = [(dtype, dm, dff, T, K, table[s % L].data_ptr(), E, ids_d[s].data_ptr(), wts_d[s].data_ptr(),
+                     xs_d[s].data_ptr(), out.data_ptr(), 0, stream) for s in range(total_steps)]
+        timed_u = distinct[args.warmup:]
+        step_bytes = int(np.mean(step_bytes_list[args.warmup:]))
+        launch_bytes = step_bytes
+
+        def run_step(s):
+            rc = fn(*all_args[s])
+            if rc:
+                mer.errors.raise_for_status(rc)
+
+        # parity sample: the experts token 0 of step 0 routes to, on its input
+        sample_experts = [int(e) for e in ids[0, 0]]
+        x_ref = xs[0, 0]
+        experts_per_step = T * K
+        routing_desc = ("N(0,1) logits + ln p_zipf(rank; s=1.1) over a seeded rank permutation, softmax top-8 "
+                        f"renormalised; distinct experts per step {timed_u.min()}..{timed_u.max()} "
+                        f"(mean {timed_u.mean():.1f})")
     else:
         table = torch.tensor([[base + (l * E + e) * ebytes for e in range(E)] for l in range(L)],
                              dtype=torch.int64, device=dev)
@@ -277,13 +320,23 @@ def main() -> int:
     # Per-launch algorithmic bytes of each stage (packed weights of each
     # distinct expert touched + f32 activations in/out).
     proj = ebytes // 3
-    stage_bytes = {
-        "decode": launch_bytes,                                       # the persistent decode kernel
-        "gate_up": K * 2 * proj + dm // 32 * 100 + K * dff // 32 * 100,
-        "down": K * proj + K * dff // 32 * 100 + K * 4 * dm * 4,
-        "combine": K * 4 * dm * 4 + 2 * dm * 4,
-        "prep": dm * 4 + dm // 32 * 100 + K * 12,
-    }
+    if args.config == 3:
+        u = float(np.mean(timed_u))
+        n_pairs = cfg["tokens"] * K
+        stage_bytes = {
+            "prep": n_pairs * 8 + cfg["tokens"] * dm * 4 + cfg["tokens"] * dm // 32 * 100,
+            "gate_up": int(u * 2 * proj) + cfg["tokens"] * dm // 32 * 100 + n_pairs * dff // 32 * 100,
+            "down": int(u * proj) + n_pairs * dff // 32 * 100 + n_pairs * dm * 4,
+            "combine": n_pairs * dm * 4 + cfg["tokens"] * dm * 4,
+        }
+    else:
+        stage_bytes = {
+            "decode": launch_bytes,  # the persistent decode kernel
+            "gate_up": K * 2 * proj + dm // 32 * 100 + K * dff // 32 * 100,
+            "down": K * proj + K * dff // 32 * 100 + K * 4 * dm * 4,
+            "combine": K * 4 * dm * 4 + 2 * dm * 4,
+            "prep": dm * 4 + dm // 32 * 100 + K * 12,
+        }
     stage_info = {}
     for name, (ms, cnt) in stages.items():
         if cnt:
@@ -294,21 +347,33 @@ def main() -> int:
 
     # GPU outputs of the sampled experts on the reference input (parity leg)
     xdev = torch.from_numpy(np.ascontiguousarray(x_ref)).to(dev)
-    gpu_y = [mer.dispatch_expert_forward(mer.WeightDtype(dtype), blob(e), xdev, dm, dff).cpu().numpy().astype(np.float64)
-             for e in sample_experts]
+    if args.config == 3:
+        # each sampled expert through the grouped path: one token per pair, weight 1
+        n_s = len(sample_experts)
+        gy = mer.moe_grouped(mer.WeightDtype(dtype), dm, dff, table[0],
+                             torch.tensor(sample_experts, dtype=torch.int32, device=dev).reshape(n_s, 1),
+                             torch.ones((n_s, 1), dtype=torch.float32, device=dev), xdev.reshape(1, dm).repeat(n_s, 1))
+        gpu_y = list(gy.cpu().numpy().astype(np.float64))
+    else:
+        gpu_y = [mer.dispatch_expert_forward(mer.WeightDtype(dtype), blob(e), xdev, dm, dff).cpu().numpy()
+                 .astype(np.float64) for e in sample_experts]
 
     config = {"workload": cfg["workload"], "layers": L, "experts_per_layer": E if args.config else 1,
-              "top_k": K, "d_model": dm, "d_ff": dff, "weights": "Q4_0" if dtype == Q4 else "Q8_0", "batch": 1,
+              "top_k": K, "d_model": dm, "d_ff": dff, "weights": "Q4_0" if dtype == Q4 else "Q8_0",
+              "batch": cfg.get("tokens", 1),
               "resident_bytes": n_exp * ebytes, "bytes_per_step": step_bytes, "parallelism": "single-gpu",
               "routing": routing_desc}
-    if args.config:
+    if args.config == 3:
+        config["launch"] = "mer_hip_moe_grouped per step (group, gate/up, down, combine)"
+        config["layer_copies"] = "steps cycle over the 8 copies; each step reads one copy's routed experts"
+    elif args.config:
         config["launch"] = "per-layer" if args.per_layer else "all-layers"
         config["routing_use"] = ("each layer's routing used only after the previous layer's output is complete"
                                  if args.per_layer or args.route_after_prev else
                                  "every layer's routing is a launch input")
     result = {
         "metric": cfg["metric"],
-        "value": steps_per_s,
+        "value": steps_per_s * cfg.get("tokens", 1),
         "unit": cfg["unit"],
         "n_gpus": 1,
         "steps": args.steps,
@@ -320,9 +385,10 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic",
         "config": config,
-        "hbm_gbps": step_bytes * steps_per_s / 1e9,
+        "hbm_gbps": step_bytes * steps_per_s / 1e9,  # algorithmic bytes per step x steps/s
         "hbm_frac_of_peak": step_bytes * steps_per_s / 1e9 / HBM_PEAK_GBPS,
-        "roofline": {"bound": "hbm", "kernel": "decode_kernel" if dominant == "decode" else f"proj_kernel ({dominant})",
+        "roofline": {"bound": "hbm", "kernel": "decode_kernel" if dominant == "decode" else
+                     (f"gproj_kernel ({dominant})" if args.config == 3 else f"proj_kernel ({dominant})"),
                      "achieved": dom["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": dom["gbps"] / HBM_PEAK_GBPS, "traffic": None,
                      "algorithmic_bytes_per_launch": stage_bytes[dominant], "avg_launch_us": dom["avg_us"]},
