@@ -114,8 +114,10 @@ int mer_hip_stage_timing_read(double *ms /*[MER_STAGE_COUNT]*/, uint64_t *counts
 /* Item trace of the persistent decode kernel (tracing aid, no reference
  * counterpart): while set, every launch writes for item i, at record i of
  * d_records (8 x uint64: item << 32 | XCC id << 16 | low 16 bits of HW_ID,
- * start, inputs ready, digits fetched, walk done, arrived, end, 0; wall-clock
- * ticks of *clock_khz kHz, 0 = mark not reached).  NULL disables. */
+ * start, inputs ready, digits fetched, walk done, arrived, end, combined
+ * (the D item that combined a tile: its sum stored and the next layer's
+ * input block packed); wall-clock ticks of *clock_khz kHz, 0 = mark not
+ * reached).  NULL disables. */
 int mer_hip_decode_trace(void *d_records, size_t capacity, uint64_t *clock_khz);
 
 /* ---- host-only sizing and validation (no GPU work) ----------------- */

@@ -69,6 +69,8 @@ struct DeviceState {
   size_t scratch_floats = 0;
   uint32_t *counters = nullptr;  // decode counters, all zero between launches
   size_t counter_words = 0;
+  uint32_t *release = nullptr;   // decode release flags (epoch-valued, zero at allocation)
+  size_t release_words = 0;
   uint32_t *status = nullptr;
   uint64_t clock_khz = 100000;
   uint64_t *trace = nullptr;     // decode item trace buffer (caller-owned)
@@ -174,6 +176,32 @@ int ensure_counters(size_t words, hipStream_t st, uint32_t **out) {
     d.counter_words = want;
   }
   *out = d.counters;
+  return MER_OK;
+}
+
+// Release flags: zeroed once when (re)allocated, never cleared by kernels
+// (they hold launch epochs, and every launch has a newer one).
+int ensure_release(size_t words, hipStream_t st, uint32_t **out) {
+  DeviceState &d = g_dev[g_device];
+  if (d.release_words < words) {
+    if (capturing(st))
+      return fail(MER_ERR_PHYSICAL_CAPACITY, "decode release flags must grow, which cannot happen under graph capture: "
+                                             "run the same call once before capturing");
+    if (d.release) {
+      hipError_t e = hipDeviceSynchronize();
+      if (e != hipSuccess) return hip_fail(e, MER_ERR_DEVICE_LOST, "synchronise before release-flag growth");
+      (void)hipFree(d.release);
+      d.release = nullptr;
+      d.release_words = 0;
+    }
+    size_t want = words < (1u << 16) ? (1u << 16) : words;
+    hipError_t e = hipMalloc(&d.release, want * 4);
+    if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "decode release-flag allocation");
+    e = hipMemset(d.release, 0, want * 4);
+    if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "decode release-flag initialisation");
+    d.release_words = want;
+  }
+  *out = d.release;
   return MER_OK;
 }
 
@@ -288,6 +316,7 @@ int run_decode(int dtype, size_t dm, size_t dff, uint32_t n_layers, uint32_t n_t
   p.d_tiles = (uint32_t)(dm / kTileRows);
   const uint32_t pack_blocks = fmt == FMT_Q4_0 ? 16 : 8;
   p.p_items = (uint32_t)div_ceil(p.xblocks, pack_blocks);
+  p.combine_packs = 1u;
   p.off_p = n_tok;
   p.off_g = p.off_p + n_tok * p.p_items;
   p.off_d = p.off_g + p.n_inst * p.g_slices * p.g_tiles;
@@ -329,6 +358,9 @@ int run_decode(int dtype, size_t dm, size_t dff, uint32_t n_layers, uint32_t n_t
   uint32_t *counters = nullptr;
   if ((rc = ensure_counters(p.n_counters, st, &counters))) return rc;
   p.counters = counters;
+  uint32_t *release = nullptr;
+  if ((rc = ensure_release((size_t)n_layers * n_tok * kReleaseFan * kPollStride, st, &release))) return rc;
+  p.release = release;
   p.exit_count = counters + dev.counter_words - 1;
   p.abort_flag = counters + dev.counter_words - kPollStride;
   p.status = dev.status;
@@ -644,6 +676,7 @@ int mer_hip_shutdown(void) {
   (void)hipDeviceSynchronize();
   if (d.scratch) (void)hipFree(d.scratch);
   if (d.counters) (void)hipFree(d.counters);
+  if (d.release) (void)hipFree(d.release);
   d = DeviceState{};
   g_device = -1;
   return MER_OK;

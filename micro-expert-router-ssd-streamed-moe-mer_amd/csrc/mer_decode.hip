@@ -6,14 +6,20 @@
 // one-wave workgroups walks a global list of work items, layer by layer:
 //   R  check a token's expert slots (ids -> table) and report residency
 //      misses; G and D items look their blob up themselves
-//   P  quantise 16 (Q4_0) / 8 (Q8_0) blocks of a token's layer input into
-//      digit planes
+//   P  quantise 16 (Q4_0) / 8 (Q8_0) blocks of a token's layer-0 input into
+//      digit planes (idle in later layers: their input blocks are packed by
+//      the combines of the layer before)
 //   G  gate/up of one (slot, column slice, 32-row tile): streams the tile's
 //      gate and up rows; with one slice it applies SiLU and packs the tile
 //      of h into digit planes, otherwise the last slice to arrive does
 //   D  down of one (slot, column slice, 32-row tile) -> partial sums; the
 //      last (slot, slice) to arrive for a (token, tile) combines
 //      out = [x +] sum_i w_i y_i for the tile (combine_outputs_into order)
+//      and packs the same 32 elements of the next layer's input (that
+//      output when chained, else the caller's next x) into digit planes;
+//      the last combine of a layer sets the layer's release flags, which
+//      the next layer's items poll (each on one of 16 lines, so hundreds of
+//      waiters do not all poll the line the combines count on)
 // Dependencies are counters in global memory.  Partial sums and outputs
 // handed from one wave to another are written and read with device-scope
 // (sc1) accesses, which are coherent across the XCDs for exactly the lines
@@ -129,12 +135,18 @@ __device__ __forceinline__ bool arrive_last(uint32_t *ctr, uint32_t expected) {
   return old + 1 == expected;
 }
 
+// Release flag k of (layer, token): its own 256-byte line; holds the epoch
+// of the last launch whose layer was complete for that token.
+__device__ __forceinline__ uint32_t *release_flag(const DecodeParams &p, uint32_t layer, uint32_t t, uint32_t k) {
+  return p.release + (((size_t)layer * p.n_tok + t) * kReleaseFan + k) * kPollStride;
+}
+
 // Optional per-item trace, 8 x u64 per item: {item << 32 | XCC << 16 | low
 // HW_ID bits, start, inputs ready, digits fetched, walk done, arrived
-// (D items), end, 0} in wall-clock ticks (records beyond trace_cap are
-// dropped; unset marks are 0).
+// (D items), end, combined (combining D items)} in wall-clock ticks
+// (records beyond trace_cap are dropped; unset marks are 0).
 struct TraceMarks {
-  uint64_t start, ready, fetched, walked, arrived;
+  uint64_t start, ready, fetched, walked, arrived, extra;
 };
 __device__ __forceinline__ uint64_t trace_now(const DecodeParams &p) { return p.trace ? wall_clock64() : 0; }
 __device__ __forceinline__ void trace_item(const DecodeParams &p, uint64_t gi, const TraceMarks &m) {
@@ -150,14 +162,30 @@ __device__ __forceinline__ void trace_item(const DecodeParams &p, uint64_t gi, c
   r[4] = m.walked;
   r[5] = m.arrived;
   r[6] = wall_clock64();
-  r[7] = 0;
+  r[7] = m.extra;
 }
 
+// Sum of v over each group of G adjacent lanes (G = 16, 32 or 64), on every
+// lane of the group.  Row sums (16 lanes) take four DPP row rotations,
+// which cost a VALU op each; rows are then combined through readlane
+// (uniform values) instead of LDS-routed lane permutes.
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128 /* row_ror:8 */, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124 /* row_ror:4 */, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x122 /* row_ror:2 */, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x121 /* row_ror:1 */, 0xf, 0xf, false));
+  if constexpr (G == 16) {
+    return v;
+  } else {
+    const int b = __float_as_int(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+    if constexpr (G == 32) return (threadIdx.x & 32u) ? r2 + r3 : r0 + r1;
+    else return (r0 + r1) + (r2 + r3);
+  }
 }
 
 // Quantise `nblocks` (<= 64 / groups) blocks of x into digit planes in line
@@ -376,16 +404,27 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
     uint32_t *hq_dig = p.hq_dig + (size_t)l * p.n_inst * p.hblocks * kLineDwords;
     // layer input of token t
     const float *xsrc = (p.flags & kFlagChain) && l > 0 ? p.layers[l - 1].out : la.x;
-    // Layer l-1's output for token t is complete (its combine counter).
+    // Layer l-1's output for token t is complete: the last of its combines
+    // has set the layer's release flags to this launch's epoch.  A waiter
+    // polls one of kReleaseFan flags (by item), so hundreds of waiting waves
+    // do not all poll the line the combines count on.
     auto wait_prev_layer = [&](uint32_t t) {
-      if (l > 0) wait_for(p, p.counters + (size_t)(l - 1) * p.cnt_per_layer + p.c_c + (size_t)t * kPollStride, p.d_tiles);
+      if (l > 0) wait_for(p, release_flag(p, l - 1, t, (uint32_t)(gi % kReleaseFan)), p.epoch);
     };
     const bool route_after_prev = (p.flags & kFlagRouteAfterPrev) != 0;
+    // Layer l's input digits of token t are complete.  Layer 0's are packed
+    // by its P items; with combine packing, layer l > 0's input block b is
+    // packed by the combine of tile b of layer l-1, so all of them are there
+    // once every tile of layer l-1 is combined.
+    auto wait_input = [&](uint32_t t) {
+      if (l > 0 && p.combine_packs) wait_prev_layer(t);
+      else wait_for(p, cnt + p.c_p + (size_t)t * kPollStride, p.p_items);
+    };
     // Under ROUTE_AFTER_PREV, G and D items touch their experts only once the
     // layer's input is packed (which implies layer l-1 is complete), so the
     // input packing does not queue behind every wave's weight prefetch.
     auto wait_input_packed = [&](uint32_t t) {
-      if (l > 0) wait_for(p, cnt + p.c_p + (size_t)t * kPollStride, p.p_items);
+      if (l > 0) wait_input(t);
     };
 
     if (j < p.off_p) {
@@ -407,6 +446,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       const uint32_t idx = j - p.off_p;
       const uint32_t t = idx / p.p_items;
       const uint32_t part = idx % p.p_items;
+      if (l > 0 && p.combine_packs) continue;  // packed by layer l-1's combines
       wait_prev_layer(t);  // layers run in order: layer l reads after layer l-1 wrote
       tm.ready = trace_now(p);
       const uint32_t b0 = part * kPackBlocks;
@@ -435,7 +475,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       walk.init(bases, p.g_chunks * (uint32_t)FmtTraits<FMT>::kChunkBytes, c, valid, tile * kTileRows + grp * 2);
       typename W::WBuf wbuf[kBuffers];
       walk.prefetch(wbuf);
-      wait_for(p, cnt + p.c_p + (size_t)t * kPollStride, p.p_items);
+      wait_input(t);
       tm.ready = trace_now(p);
       uint32_t xd[2 * kBlockDigitDwords];
       float xsc[2];
@@ -549,8 +589,19 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
           }
           const float val = (p.flags & (kFlagResidual | kFlagAccumulate)) ? base + acc : acc;
           st_dev(o, val);
+          if (p.combine_packs && l + 1 < p.n_layers)
+            s_h[lane] = (p.flags & kFlagChain) ? val : p.layers[l + 1].x[(size_t)t * p.d_model + r];
         }
-        signal(cnt + p.c_c + (size_t)t * kPollStride);
+        if (p.combine_packs && l + 1 < p.n_layers) {
+          // block `tile` of layer l+1's input, the tile just combined (chained)
+          // or the caller's next input, into layer l+1's digit lines
+          __syncthreads();
+          uint32_t *next_dig = p.xq_dig + ((size_t)(l + 1) * p.n_tok * p.xblocks + (size_t)t * p.xblocks + tile) * kLineDwords;
+          pack_blocks<FMT, false>(s_h, 1, next_dig, p.epoch);
+        }
+        tm.extra = trace_now(p);
+        if (arrive_last(cnt + p.c_c + (size_t)t * kPollStride, p.d_tiles) && lane < kReleaseFan)
+          st_dev(release_flag(p, l, t, lane), p.epoch);
         compiler_fence();
       }
     }

@@ -88,6 +88,7 @@ constexpr uint32_t kFlagRouteAfterPrev = 8u;  // layer l > 0 touches its experts
 constexpr uint32_t kMaxLayers = 64;
 constexpr uint32_t kLineDwords = 32;     // decode digit block: 24 digit dwords, scale, padding
 constexpr uint32_t kPollStride = 64;     // words between polled decode counters (one 256-byte line each)
+constexpr uint32_t kReleaseFan = 16;     // release flags per (layer, token), one line each
 
 struct LayerArgs {
   const void *const *table;  // device array of expert blob pointers
@@ -108,6 +109,7 @@ struct DecodeParams {
   uint32_t g_chunks, g_slices, g_cps, g_tiles;  // gate/up: chunks per row, slices, chunks per slice, tiles
   uint32_t d_chunks, d_slices, d_cps, d_tiles;  // down
   uint32_t p_items;          // packing items per token
+  uint32_t combine_packs;    // layer l > 0's input is packed by layer l-1's combines (P items idle)
   uint32_t items_per_layer, off_p, off_g, off_d;
   uint64_t total_items;
   // scratch, all [layer]-major
@@ -122,6 +124,7 @@ struct DecodeParams {
   uint32_t *counters;        // [L][cnt_per_layer], zero between launches
   uint32_t cnt_per_layer, c_p, c_ga, c_gd, c_da, c_c;
   uint32_t n_counters;
+  uint32_t *release;         // [L][n_tok][kReleaseFan] epoch flags (never cleared: older epochs read as not set)
   uint32_t *exit_count;
   uint32_t *abort_flag;      // set by a timed-out wait; later waits give up
   uint32_t *status;
