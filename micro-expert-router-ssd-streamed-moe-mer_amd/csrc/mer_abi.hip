@@ -358,9 +358,16 @@ int run_decode(int dtype, size_t dm, size_t dff, uint32_t n_layers, uint32_t n_t
   uint32_t *counters = nullptr;
   if ((rc = ensure_counters(p.n_counters, st, &counters))) return rc;
   p.counters = counters;
+  // Release flags of layers, and of h slices when their count is small
+  // (each flag takes a 256-byte line).
+  const size_t layer_flags = (size_t)n_layers * n_tok * kReleaseFan * kPollStride;
+  const size_t gd_keys = (size_t)n_layers * p.n_inst * p.d_slices;
+  const bool gd_fan = gd_keys <= 1024;
+  const size_t gd_flags = gd_fan ? gd_keys * kReleaseFan * kPollStride : 0;
   uint32_t *release = nullptr;
-  if ((rc = ensure_release((size_t)n_layers * n_tok * kReleaseFan * kPollStride, st, &release))) return rc;
+  if ((rc = ensure_release(layer_flags + gd_flags, st, &release))) return rc;
   p.release = release;
+  p.gd_release = gd_fan ? release + layer_flags : nullptr;
   p.exit_count = counters + dev.counter_words - 1;
   p.abort_flag = counters + dev.counter_words - kPollStride;
   p.status = dev.status;

@@ -19,7 +19,9 @@
 //      output when chained, else the caller's next x) into digit planes;
 //      the last combine of a layer sets the layer's release flags, which
 //      the next layer's items poll (each on one of 16 lines, so hundreds of
-//      waiters do not all poll the line the combines count on)
+//      waiters do not all poll the line the combines count on); likewise the
+//      last h tile of a column slice releases the slice's D items when the
+//      number of slices is small
 // Dependencies are counters in global memory.  Partial sums and outputs
 // handed from one wave to another are written and read with device-scope
 // (sc1) accesses, which are coherent across the XCDs for exactly the lines
@@ -139,6 +141,13 @@ __device__ __forceinline__ bool arrive_last(uint32_t *ctr, uint32_t expected) {
 // of the last launch whose layer was complete for that token.
 __device__ __forceinline__ uint32_t *release_flag(const DecodeParams &p, uint32_t layer, uint32_t t, uint32_t k) {
   return p.release + (((size_t)layer * p.n_tok + t) * kReleaseFan + k) * kPollStride;
+}
+
+// Release flag k of the h slice (layer, instance, column slice), set when
+// all of the slice's h tiles are packed.
+__device__ __forceinline__ uint32_t *gd_flag(const DecodeParams &p, uint32_t layer, uint32_t inst, uint32_t ds,
+                                             uint32_t k) {
+  return p.gd_release + ((((size_t)layer * p.n_inst + inst) * p.d_slices + ds) * kReleaseFan + k) * kPollStride;
 }
 
 // Optional per-item trace, 8 x u64 per item: {item << 32 | XCC << 16 | low
@@ -513,7 +522,14 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
         __syncthreads();
         const size_t hb = (size_t)inst * p.hblocks + tile;
         pack_blocks<FMT, false>(s_h, 1, hq_dig + hb * kLineDwords, p.epoch);
-        signal(cnt + p.c_gd + ((size_t)inst * p.d_slices + dslice) * kPollStride);
+        uint32_t *gd = cnt + p.c_gd + ((size_t)inst * p.d_slices + dslice) * kPollStride;
+        if (p.gd_release) {
+          // the last h tile of the slice releases its D items
+          const uint32_t tiles = min(p.d_cps * 2, p.g_tiles - dslice * p.d_cps * 2);
+          if (arrive_last(gd, tiles) && lane < kReleaseFan) st_dev(gd_flag(p, l, inst, dslice, lane), p.epoch);
+        } else {
+          signal(gd);
+        }
       }
     } else {
       // ---- D: down of one (slot, column slice, tile) + combine -------------
@@ -540,7 +556,8 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       // the h planes of this column slice
       const uint32_t first_tile = ds * p.d_cps * 2;
       const uint32_t n_tiles = min(p.d_cps * 2, p.g_tiles - first_tile);
-      wait_for(p, cnt + p.c_gd + ((size_t)inst * p.d_slices + ds) * kPollStride, n_tiles);
+      if (p.gd_release) wait_for(p, gd_flag(p, l, inst, ds, (uint32_t)(gi % kReleaseFan)), p.epoch);
+      else wait_for(p, cnt + p.c_gd + ((size_t)inst * p.d_slices + ds) * kPollStride, n_tiles);
       tm.ready = trace_now(p);
       uint32_t xd[2 * kBlockDigitDwords];
       float xsc[2];
@@ -557,7 +574,18 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       walk.run(wbuf, xd, xsc, emit);
       tm.walked = trace_now(p);
       __syncthreads();
+      // What a combine of this tile adds to the sum is already final: the
+      // residual or accumulated output (written by layer l-1, complete before
+      // any item of this layer ran) and the caller's next-layer input.  Every
+      // D item loads it now, so the drain of its arrival covers the latency
+      // and the combine waits on one round trip only.
+      const bool pack_next = p.combine_packs && l + 1 < p.n_layers;
+      float base = 0.f, next_x = 0.f;
       if (lane < kTileRows) {
+        const uint32_t r = tile * kTileRows + lane;
+        if (p.flags & kFlagResidual) base = ld_dev(xsrc + (size_t)t * p.d_model + r);
+        else if (p.flags & kFlagAccumulate) base = ld_dev(la.out + (size_t)t * p.d_model + r);
+        if (pack_next && !(p.flags & kFlagChain)) next_x = p.layers[l + 1].x[(size_t)t * p.d_model + r];
         const float y = s_h[lane];
         st_dev(part + tile * kTileRows + lane, (la.weights && w_slot == 0.0f) ? 0.0f : w_slot * y);
       }
@@ -571,9 +599,6 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
         if (lane < kTileRows) {
           const uint32_t r = tile * kTileRows + lane;
           float *o = la.out + (size_t)t * p.d_model + r;
-          float base = 0.f;
-          if (p.flags & kFlagResidual) base = ld_dev(xsrc + (size_t)t * p.d_model + r);
-          else if (p.flags & kFlagAccumulate) base = ld_dev(o);
           const uint32_t n_parts = p.top_k * p.d_slices;
           const float *pp = p.partial + ((size_t)l * p.n_inst + (size_t)t * p.top_k) * p.d_slices * p.d_model + r;
           float acc = 0.f;
@@ -589,10 +614,9 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
           }
           const float val = (p.flags & (kFlagResidual | kFlagAccumulate)) ? base + acc : acc;
           st_dev(o, val);
-          if (p.combine_packs && l + 1 < p.n_layers)
-            s_h[lane] = (p.flags & kFlagChain) ? val : p.layers[l + 1].x[(size_t)t * p.d_model + r];
+          if (pack_next) s_h[lane] = (p.flags & kFlagChain) ? val : next_x;
         }
-        if (p.combine_packs && l + 1 < p.n_layers) {
+        if (pack_next) {
           // block `tile` of layer l+1's input, the tile just combined (chained)
           // or the caller's next input, into layer l+1's digit lines
           __syncthreads();

@@ -125,6 +125,7 @@ struct DecodeParams {
   uint32_t cnt_per_layer, c_p, c_ga, c_gd, c_da, c_c;
   uint32_t n_counters;
   uint32_t *release;         // [L][n_tok][kReleaseFan] epoch flags (never cleared: older epochs read as not set)
+  uint32_t *gd_release;      // [L][n_inst][d_slices][kReleaseFan] h-slice release flags, or null (counters)
   uint32_t *exit_count;
   uint32_t *abort_flag;      // set by a timed-out wait; later waits give up
   uint32_t *status;
