@@ -428,14 +428,23 @@ def main() -> int:
     torch.cuda.synchronize()
     mer.take_device_status()
 
+    # Config 3 issues four launches per step: its value is timed without the
+    # per-launch stage events, which then run over a second pass of the same
+    # steps.  Elsewhere the events bracket the kernel inside the timed region.
+    separate_stage_pass = args.config == 3
     log(f"timing {args.steps} steps")
-    mer.stage_timing_enable(True)
+    mer.stage_timing_enable(not separate_stage_pass)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.warmup, total_steps):
         run_step(s)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    if separate_stage_pass:
+        mer.stage_timing_enable(True)
+        for s in range(args.warmup, total_steps):
+            run_step(s)
+        torch.cuda.synchronize()
     stages = mer.stage_timing_read()
     mer.stage_timing_enable(False)
     mer.take_device_status()

@@ -596,13 +596,14 @@ int run_grouped(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
   auto up64 = [](size_t v) { return (v + 63) / 64 * 64; };  // floats; 256-byte aligned regions
   const size_t n_hdr = 64;
   const size_t n_plist = up64(p.n_pairs);
+  const size_t n_ok = up64(p.n_pairs);
   const size_t n_tiles = up64((size_t)max_tiles * sizeof(GroupTile) / 4);
   const size_t n_xg = up64((size_t)n_tokens * p.xblocks * 24);
   const size_t n_xs = up64((size_t)n_tokens * p.xblocks);
   const size_t n_hg = up64((size_t)p.n_pairs * p.hblocks * 24);
   const size_t n_hs = up64((size_t)p.n_pairs * p.hblocks);
   const size_t n_pa = up64((size_t)p.n_pairs * dm);
-  const size_t total = n_hdr + n_plist + n_tiles + n_xg + n_xs + n_hg + n_hs + n_pa;
+  const size_t total = n_hdr + n_plist + n_ok + n_tiles + n_xg + n_xs + n_hg + n_hs + n_pa;
   if (dev.scratch_floats < total && capturing(st))
     return fail(MER_ERR_PHYSICAL_CAPACITY,
                 "scratch must grow, which cannot happen under graph capture: run the same call once before capturing");
@@ -613,6 +614,8 @@ int run_grouped(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
   cur += n_hdr;
   p.plist = reinterpret_cast<uint32_t *>(cur);
   cur += n_plist;
+  p.pair_ok = reinterpret_cast<uint32_t *>(cur);
+  cur += n_ok;
   p.tiles = reinterpret_cast<GroupTile *>(cur);
   cur += n_tiles;
   p.xg = reinterpret_cast<uint32_t *>(cur);

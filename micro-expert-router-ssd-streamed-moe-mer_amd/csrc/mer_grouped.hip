@@ -53,6 +53,9 @@ constexpr uint32_t kGTok = 16;           // pairs per token tile (MFMA N)
 constexpr uint32_t kGRows = 64;          // weight rows staged per workgroup
 constexpr uint32_t kGStageBlocks = 16;   // K blocks per LDS stage
 constexpr uint32_t kGRowStride = kGStageBlocks * 32 + 16;  // LDS bytes per staged row
+// Scales are stored [block][row] with a padded row of 68 floats: the eight
+// threads that stage one row's chunks write 8 different banks.
+constexpr uint32_t kGScaleStride = kGRows + 4;
 constexpr float kGIntMax = 8355711.0f;   // |v| bound (0x7f7f7f): v + 0x808080 stays in 24 bits
 constexpr uint32_t kGRec = 6;            // dwords per (vector, block, k-group) digit record
 constexpr uint32_t kNoChunkG = 0x80000000u;
@@ -147,7 +150,9 @@ __global__ __launch_bounds__(1024) void group_kernel(GroupedParams p) {
   __syncthreads();
   for (uint32_t q = tid; q < p.n_pairs; q += nth) {
     const uint8_t *blob = nullptr;
-    if (pair_valid(p, q, &blob)) {
+    const bool ok = pair_valid(p, q, &blob);
+    p.pair_ok[q] = ok ? 1u : 0u;
+    if (ok) {
       pos[q] = atomicAdd(&cnt[p.ids[q]], 1u);
     } else {
       pos[q] = 0xffffffffu;
@@ -284,8 +289,8 @@ struct Stager {
       dst[1] = make_uint4(q0[4], q0[5], q0[6], q0[7]);
       dst[2] = make_uint4(q1[0], q1[1], q1[2], q1[3]);
       dst[3] = make_uint4(q1[4], q1[5], q1[6], q1[7]);
-      ld[b0 * kGRows + srow[i]] = d0;
-      ld[(b0 + 1) * kGRows + srow[i]] = d1;
+      ld[b0 * kGScaleStride + srow[i]] = d0;
+      ld[(b0 + 1) * kGScaleStride + srow[i]] = d1;
     }
   }
 };
@@ -295,9 +300,9 @@ struct Stager {
 // writes h = silu(g) * u for 32 rows = one block per pair.  Otherwise 64
 // down rows; the epilogue writes w_i * y_i per pair.
 template <int FMT, bool FUSED>
-__global__ __launch_bounds__(256) void gproj_kernel(GroupedParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void gproj_kernel(GroupedParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t lq[kGRows * kGRowStride];
-  __shared__ __attribute__((aligned(16))) float ld[kGStageBlocks * kGRows];
+  __shared__ __attribute__((aligned(16))) float ld[kGStageBlocks * kGScaleStride];
   __shared__ uint32_t s_pair[kGTok];
 
   const uint32_t row_tiles = FUSED ? p.d_ff / 32 : p.d_model / kGRows;
@@ -369,23 +374,19 @@ __global__ __launch_bounds__(256) void gproj_kernel(GroupedParams p) {
       long bk[3];
 #pragma unroll
       for (int k = 0; k < 3; ++k) bk[k] = (long)(((uint64_t)bv[j][k].y << 32) | bv[j][k].x);
-      v4i p0[4], p1[4], p2[4];
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
         const long av = *reinterpret_cast<const long *>(lq + (a * 16 + col) * kGRowStride + b * 32 + kg * 8);
         const v4i z = {0, 0, 0, 0};
-        p0[a] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[0], z, 0, 0, 0);
-        p1[a] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[1], z, 0, 0, 0);
-        p2[a] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[2], z, 0, 0, 0);
-      }
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const float4 d = *reinterpret_cast<const float4 *>(&ld[b * kGRows + a * 16 + kg * 4]);
+        const v4i p0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[0], z, 0, 0, 0);
+        const v4i p1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[1], z, 0, 0, 0);
+        const v4i p2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[2], z, 0, 0, 0);
+        const float4 d = *reinterpret_cast<const float4 *>(&ld[b * kGScaleStride + a * 16 + kg * 4]);
         const float dd[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float hi = (float)(p1[a][i] + (p2[a][i] << 8));
-          const float v = __builtin_fmaf(hi, 256.0f, (float)p0[a][i]);
+          const float hi = (float)(p1[i] + (p2[i] << 8));
+          const float v = __builtin_fmaf(hi, 256.0f, (float)p0[i]);
           acc[a][i] = __builtin_fmaf(v, dd[i] * bs[j], acc[a][i]);
         }
       }
@@ -447,7 +448,8 @@ __global__ __launch_bounds__(256) void gproj_kernel(GroupedParams p) {
 }
 
 // out[t] = [x +] sum over the token's valid slots, in slot order, of the
-// pair partials (w_i y_i).  One thread per 4 output elements.
+// pair partials (w_i y_i).  One thread per 4 output elements; the slots'
+// validity comes from the grouping kernel, so all loads are independent.
 __global__ __launch_bounds__(256) void gcombine_kernel(GroupedParams p) {
   const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
   const uint32_t per_tok = p.d_model / 4;
@@ -456,7 +458,7 @@ __global__ __launch_bounds__(256) void gcombine_kernel(GroupedParams p) {
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   for (uint32_t k = 0; k < p.top_k; ++k) {
     const uint32_t pr = t * p.top_k + k;
-    if (!pair_valid(p, pr, nullptr)) continue;
+    if (!p.pair_ok[pr]) continue;
     const float4 v = *reinterpret_cast<const float4 *>(p.partial + (size_t)pr * p.d_model + c);
     acc.x += v.x;
     acc.y += v.y;

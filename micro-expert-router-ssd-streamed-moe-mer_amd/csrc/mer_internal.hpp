@@ -162,6 +162,7 @@ struct GroupedParams {
   float *hs;                 // h block scales [n_pairs][hblocks]
   float *partial;            // w_i y_i [n_pairs][d_model]
   uint32_t *plist;           // pairs grouped by expert [n_pairs]
+  uint32_t *pair_ok;         // [n_pairs] 1 = routed to a resident expert with a nonzero weight
   GroupTile *tiles;          // [max tiles]
   uint32_t *n_tiles;         // tiles emitted by the grouping kernel
   uint32_t *status;
