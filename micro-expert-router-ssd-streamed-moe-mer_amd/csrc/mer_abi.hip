@@ -273,9 +273,10 @@ struct SliceGeom {
   int G;
   uint32_t slices, cps;
 };
-SliceGeom slice_geom(uint32_t chunks) {
+SliceGeom slice_geom(uint32_t chunks, uint32_t min_slices = 1) {
   SliceGeom g{};
   g.slices = (uint32_t)div_ceil(chunks, 64);
+  if (g.slices < min_slices) g.slices = min_slices;
   g.cps = (uint32_t)div_ceil(chunks, g.slices);
   g.G = g.cps <= 16 ? 16 : (g.cps <= 32 ? 32 : 64);
   return g;
@@ -304,7 +305,13 @@ int run_decode(int dtype, size_t dm, size_t dff, uint32_t n_layers, uint32_t n_t
   p.proj_bytes = div_ceil(dm * dff, 32) * block_bytes(dtype);
   p.xblocks = (uint32_t)(dm / 32);
   p.hblocks = (uint32_t)(dff / 32);
-  const SliceGeom gg = slice_geom((uint32_t)(dm / 64));
+  // Narrow layers (fewer than 512 gate/up items, e.g. 8 Qwen3 experts x 24
+  // tiles) split gate/up rows into two column slices, so twice as many waves
+  // stream each layer's gate and up weights (measured: 1006 -> 1111 tokens/s
+  // on the 48-layer Qwen3 decode; wider layers gain nothing).
+  const uint32_t g_chunks = (uint32_t)(dm / 64);
+  const bool narrow = (uint64_t)n_tok * top_k * (dff / kTileRows) < 512 && g_chunks >= 32;
+  const SliceGeom gg = slice_geom(g_chunks, narrow ? 2 : 1);
   const SliceGeom gd = slice_geom((uint32_t)(dff / 64));
   p.g_chunks = (uint32_t)(dm / 64);
   p.g_slices = gg.slices;
