@@ -312,7 +312,14 @@ int run_decode(int dtype, size_t dm, size_t dff, uint32_t n_layers, uint32_t n_t
   const uint32_t g_chunks = (uint32_t)(dm / 64);
   const bool narrow = (uint64_t)n_tok * top_k * (dff / kTileRows) < 512 && g_chunks >= 32;
   const SliceGeom gg = slice_geom(g_chunks, narrow ? 2 : 1);
-  const SliceGeom gd = slice_geom((uint32_t)(dff / 64));
+  // Down rows longer than 64 chunks are cut into 32-chunk slices when they
+  // divide evenly (Mixtral's 224 -> 7 x 32), so every lane of a 32-lane row
+  // group has a chunk, as long as the combine still loads all its parts in
+  // one batch (measured on the Mixtral decode: 701 -> 711 tokens/s against
+  // 4 slices of 56 chunks).
+  const uint32_t d_chunks = (uint32_t)(dff / 64);
+  const bool d32 = d_chunks > 64 && d_chunks % 32 == 0 && top_k * (d_chunks / 32) <= kCombineBatch;
+  const SliceGeom gd = slice_geom(d_chunks, d32 ? d_chunks / 32 : 1);
   p.g_chunks = (uint32_t)(dm / 64);
   p.g_slices = gg.slices;
   p.g_cps = gg.cps;

@@ -249,8 +249,7 @@ __device__ __forceinline__ void pack_blocks(const float *x, uint32_t nblocks, ui
 // reads zeros, so the load sequence is branch-free and the compiler can
 // keep exactly the next passes' loads outstanding.  `emit(row, acc[S])`
 // receives each row's sums on all lanes of the owning group.
-constexpr uint32_t kNoChunk = 0x80000000u;
-constexpr uint32_t kCombineBatch = 16;  // partial sums a combine loads in one batch  // beyond num_records: loads return 0
+constexpr uint32_t kNoChunk = 0x80000000u;  // beyond num_records: loads return 0
 
 template <int FMT, int G, int R, int S, int NB>
 struct TileWalk {

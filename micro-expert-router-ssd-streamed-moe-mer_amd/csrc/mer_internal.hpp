@@ -89,6 +89,7 @@ constexpr uint32_t kMaxLayers = 64;
 constexpr uint32_t kLineDwords = 32;     // decode digit block: 24 digit dwords, scale, padding
 constexpr uint32_t kPollStride = 64;     // words between polled decode counters (one 256-byte line each)
 constexpr uint32_t kReleaseFan = 16;     // release flags per (layer, token), one line each
+constexpr uint32_t kCombineBatch = 16;   // partial sums a decode combine loads in one batch
 
 struct LayerArgs {
   const void *const *table;  // device array of expert blob pointers
