@@ -68,6 +68,7 @@ enum mer_status {
   /* library state */
   MER_ERR_NOT_INITIALIZED = 48,
   MER_ERR_WRONG_DEVICE = 49,
+  MER_ERR_IO = 50, /* a file could not be opened or read (the reference's io::Error) */
 };
 
 /* Detail of the calling thread's last failure.  For BufferTooSmall and
@@ -334,6 +335,63 @@ int mer_slot_cache_stats(mer_slot_cache *cache, mer_slot_stats *out);
  * so H2D copies run asynchronously. */
 int mer_hip_host_alloc(size_t bytes, void **out);
 int mer_hip_host_free(void *p);
+
+/* ---- on-disk expert formats (host only; no device, no mer_hip_init) ----
+ * The expert-blob headers and the GGUF reader that feed the RAM tier, so
+ * real checkpoints reach the routed forwards byte for byte. */
+
+/* UTH expert-blob headers (tensor_header.rs): a UTH1 (64 B) or UTH2
+ * (128 B, per-projection dtype ranges) header at byte 0, optionally padded
+ * to the block alignment.  mer_uth_probe strips a blob as
+ * ExpertResident::new_with_block_align does (expert_cache.rs:110-143):
+ * UTH2 first (probe + range validation), then UTH1, else a headerless
+ * (legacy) blob, which is not an error (kind 0, payload = the whole blob). */
+typedef struct mer_uth_projection {
+  int32_t dtype;   /* UthDtypeId: 4 = Q4_0, 5 = Q8_0, ... */
+  uint32_t weights;
+  uint64_t offset; /* from the payload start */
+  uint64_t len;
+} mer_uth_projection;
+typedef struct mer_uth_info {
+  int32_t kind;              /* 0 headerless, 1 UTH1, 2 UTH2 */
+  int32_t dtype;             /* UTH1 dtype id; 10 (mixed) for UTH2; -1 headerless */
+  uint32_t version, flags;
+  uint32_t shape_rank, shape[4];                  /* UTH1 */
+  uint32_t quant_scale_offset, quant_scale_count; /* UTH1 */
+  uint32_t d_model, d_ff;    /* UTH2, or a UTH1 SwiGLU expert header [d_ff, d_model, 3] */
+  mer_uth_projection proj[3];/* UTH2 gate, up, down */
+  uint64_t payload_offset;   /* bytes before the weights */
+  uint64_t payload_len;
+} mer_uth_info;
+int mer_uth_probe(const void *bytes, size_t len, size_t block_align, mer_uth_info *out);
+/* TensorHeader::for_swiglu_expert + write_padded (tensor_header.rs:398-470):
+ * writes the UTH1 header of a SwiGLU expert blob padded to block_align;
+ * *written = the payload offset.  dst = NULL only reports the size. */
+int mer_uth_write_expert_header(int dtype, size_t d_model, size_t d_ff, size_t block_align, void *dst,
+                                size_t dst_len, size_t *written);
+
+/* GGUF reader for MoE expert tensors (gguf.rs:207-295, gguf_loader.rs:
+ * 136-200, :2940-3010): versions 1-3; a layer's experts are either
+ * stacked (blk.L.ffn_{gate,up}_exps.weight [d_model, d_ff, E] and
+ * blk.L.ffn_down_exps.weight [d_ff, d_model, E], GGML order) or per expert
+ * (blk.L.ffn_{gate,up,down}.e.weight).  Only Q4_0 / Q8_0 expert tensors
+ * with d_model * d_ff a multiple of 32 are accepted: their expert slices
+ * are whole block runs, copied byte for byte into MER's gate || up ||
+ * down blob.  Metadata geometry (embedding_length, [expert_]feed_forward_
+ * length, expert_count), when present, must agree with the shapes. */
+typedef struct mer_gguf mer_gguf;
+typedef struct mer_gguf_moe_info {
+  int32_t dtype;          /* MER_DTYPE_Q4_0 / MER_DTYPE_Q8_0 */
+  int32_t layout;         /* 0 stacked, 1 per-expert tensors */
+  uint64_t d_model, d_ff, n_experts;
+  uint64_t expert_bytes;  /* mer_expert_weight_bytes(dtype, d_model, d_ff) */
+} mer_gguf_moe_info;
+int mer_gguf_open(const char *path, mer_gguf **out);
+int mer_gguf_close(mer_gguf *g);
+int mer_gguf_moe_layer(mer_gguf *g, size_t layer, mer_gguf_moe_info *out);
+/* Expert `expert` of `layer` into dst (>= expert_bytes; pinned host memory
+ * from mer_hip_host_alloc makes the later upload asynchronous). */
+int mer_gguf_read_expert(mer_gguf *g, size_t layer, size_t expert, void *dst, size_t dst_len);
 
 #ifdef __cplusplus
 }

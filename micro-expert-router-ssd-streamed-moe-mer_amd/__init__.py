@@ -44,6 +44,18 @@ from .expert import (
     take_device_status,
     validate_expert,
 )
+from .formats import (
+    DEFAULT_BLOCK_ALIGN,
+    GgufExperts,
+    MoeLayer,
+    ProjectionRange,
+    StackedLayout,
+    UthDtype,
+    UthHeader,
+    probe_uth,
+    strip_uth,
+    swiglu_expert_header,
+)
 from .slots import SlotCache, pinned_expert_buffer
 
 __all__ = [n for n in dir() if not n.startswith("_")]

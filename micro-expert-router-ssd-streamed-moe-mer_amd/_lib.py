@@ -57,6 +57,23 @@ class MerErrorInfo(ctypes.Structure):
     ]
 
 
+class MerUthProjection(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int32), ("weights", ctypes.c_uint32), ("offset", c_u64), ("len", c_u64)]
+
+
+class MerUthInfo(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int32), ("dtype", ctypes.c_int32), ("version", ctypes.c_uint32),
+                ("flags", ctypes.c_uint32), ("shape_rank", ctypes.c_uint32), ("shape", ctypes.c_uint32 * 4),
+                ("quant_scale_offset", ctypes.c_uint32), ("quant_scale_count", ctypes.c_uint32),
+                ("d_model", ctypes.c_uint32), ("d_ff", ctypes.c_uint32), ("proj", MerUthProjection * 3),
+                ("payload_offset", c_u64), ("payload_len", c_u64)]
+
+
+class MerGgufMoeInfo(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int32), ("layout", ctypes.c_int32), ("d_model", c_u64), ("d_ff", c_u64),
+                ("n_experts", c_u64), ("expert_bytes", c_u64)]
+
+
 class Status(enum.IntEnum):
     OK = 0
     BUFFER_TOO_SMALL = 1
@@ -77,6 +94,7 @@ class Status(enum.IntEnum):
     SHAPE_EXCEEDS_WORKSPACE = 33
     NOT_INITIALIZED = 48
     WRONG_DEVICE = 49
+    IO = 50
 
 
 # name -> (restype, argtypes); exactly the symbols include/mer_hip.h declares.
@@ -121,6 +139,12 @@ SIGNATURES = {
     "mer_hip_host_free": (c_int, [c_void]),
     "mer_hip_fill_synthetic": (
         c_int, [c_int, c_u64, c_u64, c_u64, c_u64, c_float, c_float, c_void, c_void]),
+    "mer_uth_probe": (c_int, [c_void, c_size, c_size, ctypes.POINTER(MerUthInfo)]),
+    "mer_uth_write_expert_header": (c_int, [c_int, c_size, c_size, c_size, c_void, c_size, ctypes.POINTER(c_size)]),
+    "mer_gguf_open": (c_int, [ctypes.c_char_p, ctypes.POINTER(c_void)]),
+    "mer_gguf_close": (c_int, [c_void]),
+    "mer_gguf_moe_layer": (c_int, [c_void, c_size, ctypes.POINTER(MerGgufMoeInfo)]),
+    "mer_gguf_read_expert": (c_int, [c_void, c_size, c_size, c_void, c_size]),
 }
 
 _lock = threading.Lock()

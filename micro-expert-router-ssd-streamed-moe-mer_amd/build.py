@@ -13,7 +13,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libmer_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["mer_kernels.hip", "mer_decode.hip", "mer_router.hip", "mer_grouped.hip", "mer_slots.hip", "mer_abi.hip"]
+SOURCES = ["mer_kernels.hip", "mer_decode.hip", "mer_router.hip", "mer_grouped.hip", "mer_slots.hip", "mer_format.cpp", "mer_abi.hip"]
 HEADERS = ["mer_device.hpp", "mer_internal.hpp"]
 
 HIPCC_FLAGS = [

@@ -92,6 +92,8 @@ def raise_for_status(rc: int, layer: int = 0, expert_id: int = 0) -> None:
     status, msg, info = _lib.last_error()
     if status != rc:
         msg = msg or f"status {rc}"
+    if rc == _lib.Status.IO:  # the reference's io::Error
+        raise OSError(msg)
     if rc in _BY_STATUS:
         raise _BY_STATUS[rc](msg, have=info.have, need=info.need, d_model=info.d_model, d_ff=info.d_ff)
     try:
