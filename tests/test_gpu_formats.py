@@ -28,7 +28,7 @@ def test_gguf_experts_through_slot_cache(mer, oracle, gpu, tmp_path, ggml, dtype
             assert (info.d_model, info.d_ff, info.n_experts, int(info.dtype)) == (dm, dff, ne, dtype)
             host = [g.read_expert(layer, e, mer.pinned_expert_buffer(info.expert_bytes)) for e in range(ne)]
             blobs = [h.numpy().copy() for h in host]
-            cache = mer.SlotCache(info.dtype, dm, dff, n_slots=4, n_experts=ne)
+            cache = mer.SlotCache(info.dtype, dm, dff, n_slots=2 * T, n_experts=ne)  # T tokens x top-2 touch at most 2T experts
             ids = np.stack([rng.choice(ne, k, replace=False) for _ in range(T)]).astype(np.int32)
             w = rng.random((T, k)).astype(np.float32)
             x = rng.standard_normal((T, dm)).astype(np.float32)
