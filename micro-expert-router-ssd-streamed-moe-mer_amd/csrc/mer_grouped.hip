@@ -350,14 +350,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
     for (int i = 0; i < 4; ++i) acc[a][i] = 0.f;
 
   const uint32_t n_stages = (kblocks + kGStageBlocks - 1) / kGStageBlocks;
-  for (uint32_t s = 0; s < n_stages; ++s) {
-    sg.store(lq, ld);
-    __syncthreads();
-    if (s + 1 < n_stages) sg.load(s + 1, row_chunks, FUSED);
+  // B operands of this wave's blocks of stage s (wave, wave + 4, wave + 8,
+  // wave + 12), loaded one stage ahead: the loads of stage s + 1 are issued
+  // right after stage s's MFMAs, so they arrive during the slab store.
+  uint2 bv[4][3];
+  float bs[4];
+  auto load_b = [&](uint32_t s) {
     const uint32_t nb = min(kGStageBlocks, kblocks - s * kGStageBlocks);
-    // this wave's blocks of the stage: wave, wave + 4, wave + 8, wave + 12
-    uint2 bv[4][3];
-    float bs[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t b = wave + 4 * j;
@@ -367,6 +366,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
       for (int k = 0; k < 3; ++k) bv[j][k] = ok ? vdig[(size_t)gb * 2 * kGRec + k] : make_uint2(0, 0);
       bs[j] = ok ? vsc[gb] : 0.f;
     }
+  };
+  load_b(0);
+  for (uint32_t s = 0; s < n_stages; ++s) {
+    sg.store(lq, ld);
+    __syncthreads();
+    if (s + 1 < n_stages) sg.load(s + 1, row_chunks, FUSED);
+    const uint32_t nb = min(kGStageBlocks, kblocks - s * kGStageBlocks);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t b = wave + 4 * j;
@@ -391,6 +397,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
         }
       }
     }
+    if (s + 1 < n_stages) load_b(s + 1);
     __syncthreads();  // LDS slab consumed before the next store
   }
 
