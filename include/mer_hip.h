@@ -186,6 +186,21 @@ int mer_hip_moe_forward(int dtype, size_t d_model, size_t d_ff,
                         const float *d_x, float *d_out, unsigned flags,
                         void *stream);
 
+/* The GPU backend's f16-view entry points: Backend::expert_matmul /
+ * routed_expert_matmul (backend/mod.rs:1095-1103, :4421-4441) for one
+ * expert and routed_expert_matmul_batch_q4 (backend/mod.rs:3770-3850,
+ * :4401-4418) for a layer batch.  Every expert d_expert_ids[i] (an index
+ * into d_expert_table, as for mer_hip_moe_forward) runs on the same f16
+ * hidden state d_x [d_model]; d_out [n_experts][d_model] receives each
+ * expert's own y, rounded to f16, with no combine.  The reference's batch
+ * takes exactly 8 experts and reports any other count as ineligible; this
+ * entry point takes any count from 1 (n_experts = 1 is expert_matmul).
+ * Errors as mer_hip_moe_forward; a missing expert is recorded in the
+ * device status and gives a zero row. */
+int mer_hip_expert_batch_f16(int dtype, size_t d_model, size_t d_ff, size_t n_experts,
+                             const void *const *d_expert_table, size_t table_len, const int32_t *d_expert_ids,
+                             const uint16_t *d_x, uint16_t *d_out, void *stream);
+
 /* Grouped path for multi-token batches (prefill): the same contract as
  * mer_hip_moe_forward -- per token out = [x +] sum_i w_i y_i in slot order,
  * zero-weight slots skipped, misses recorded in the device status -- but

@@ -29,6 +29,7 @@ from .expert import (
     dequantize_to_f32,
     dispatch_expert_forward,
     expert_forward_host,
+    expert_matmul,
     expert_weight_bytes_for,
     fill_synthetic,
     forward_q8_0_direct_into,
@@ -39,6 +40,7 @@ from .expert import (
     q4_0_forward,
     q4_0_matvec,
     routed_expert_gpu_compatibility,
+    routed_expert_matmul_batch,
     stage_timing_enable,
     stage_timing_read,
     take_device_status,

@@ -123,6 +123,8 @@ SIGNATURES = {
     "mer_hip_moe_grouped": (
         c_int, [c_int, c_size, c_size, c_size, c_size, c_void, c_size, c_void, c_void, c_void, c_void,
                 ctypes.c_uint, c_void]),
+    "mer_hip_expert_batch_f16": (
+        c_int, [c_int, c_size, c_size, c_size, c_void, c_size, c_void, c_void, c_void, c_void]),
     "mer_hip_moe_forward_layers": (
         c_int, [c_int, c_size, c_size, c_size, c_size, c_size, ctypes.POINTER(MerLayerArgs), ctypes.c_uint, c_void]),
     "mer_hip_route_linear_gate": (

@@ -67,6 +67,8 @@ struct DeviceState {
   int cus = 256;
   float *scratch = nullptr;
   size_t scratch_floats = 0;
+  float *stage = nullptr;        // f32 x and y of the f16-view entry point
+  size_t stage_floats = 0;
   uint32_t *counters = nullptr;  // decode counters, all zero between launches
   size_t counter_words = 0;
   uint32_t *release = nullptr;   // decode release flags (epoch-valued, zero at allocation)
@@ -699,6 +701,7 @@ int mer_hip_shutdown(void) {
   DeviceState &d = g_dev[g_device];
   (void)hipDeviceSynchronize();
   if (d.scratch) (void)hipFree(d.scratch);
+  if (d.stage) (void)hipFree(d.stage);
   if (d.counters) (void)hipFree(d.counters);
   if (d.release) (void)hipFree(d.release);
   d = DeviceState{};
@@ -892,6 +895,51 @@ int mer_hip_moe_forward(int dtype, size_t d_model, size_t d_ff, size_t n_tokens,
     return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
   return run_experts(dtype, d_model, d_ff, (uint32_t)n_tokens, (uint32_t)top_k, d_expert_table, (uint32_t)table_len,
                      d_expert_ids, nullptr, d_weights, d_x, d_out, flags, (hipStream_t)stream, false);
+}
+
+int mer_hip_expert_batch_f16(int dtype, size_t d_model, size_t d_ff, size_t n_experts,
+                             const void *const *d_expert_table, size_t table_len, const int32_t *d_expert_ids,
+                             const uint16_t *d_x, uint16_t *d_out, void *stream) {
+  int rc = require_init();
+  if (rc) return rc;
+  if (dtype != MER_DTYPE_Q4_0 && dtype != MER_DTYPE_Q8_0)
+    return fail(MER_ERR_UNSUPPORTED_DTYPE, "unsupported expert dtype %d", dtype);
+  rc = mer_routed_expert_gpu_compatibility(dtype, d_model, d_ff);
+  if (rc) return rc;
+  if (d_model == 0 || d_ff == 0) return fail(MER_ERR_INVALID_LAYOUT, "expert dimensions must be non-zero");
+  if (n_experts == 0) return MER_OK;
+  if (n_experts > (1u << 16) || table_len > UINT32_MAX)
+    return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "too many experts in one batch");
+  if (!d_expert_table || !d_expert_ids || !d_x || !d_out) return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
+  // Each expert is a one-slot token of weight 1 on its own copy of x, so
+  // the routed forward's output row i is y of expert i, uncombined.
+  const hipStream_t st = (hipStream_t)stream;
+  DeviceState &d = g_dev[g_device];
+  const size_t need = 2 * n_experts * d_model;
+  if (d.stage_floats < need) {
+    if (capturing(st))
+      return fail(MER_ERR_PHYSICAL_CAPACITY, "the f16 staging buffer must grow, which cannot happen under graph "
+                                             "capture: run the same call once before capturing");
+    if (d.stage) {
+      hipError_t e = hipDeviceSynchronize();
+      if (e != hipSuccess) return hip_fail(e, MER_ERR_DEVICE_LOST, "synchronise before staging growth");
+      (void)hipFree(d.stage);
+      d.stage = nullptr;
+      d.stage_floats = 0;
+    }
+    hipError_t e = hipMalloc(&d.stage, need * sizeof(float));
+    if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "f16 staging allocation");
+    d.stage_floats = need;
+  }
+  float *x32 = d.stage, *y32 = d.stage + n_experts * d_model;
+  hipError_t e = launch_f16_in(d_x, d_model, n_experts, x32, st);
+  if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "f16 input staging launch");
+  rc = run_experts(dtype, d_model, d_ff, (uint32_t)n_experts, 1u, d_expert_table, (uint32_t)table_len, d_expert_ids,
+                   nullptr, nullptr, x32, y32, 0u, st, false);
+  if (rc) return rc;
+  e = launch_f16_out(y32, n_experts * d_model, d_out, st);
+  if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "f16 output staging launch");
+  return MER_OK;
 }
 
 int mer_hip_moe_grouped(int dtype, size_t d_model, size_t d_ff, size_t n_tokens, size_t top_k,

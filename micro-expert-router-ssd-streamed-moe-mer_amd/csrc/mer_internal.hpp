@@ -208,6 +208,8 @@ hipError_t launch_q4_raw(const uint8_t *w, size_t w_block_off, uint32_t rows, ui
                          const float *x, float *y, hipStream_t st);
 hipError_t launch_fill(int fmt, uint64_t seed, uint64_t expert, uint64_t block_begin, uint64_t n_blocks,
                        float lo, float hi, uint8_t *dst, hipStream_t st);
+hipError_t launch_f16_in(const uint16_t *x, size_t d_model, size_t n_rep, float *dst, hipStream_t st);
+hipError_t launch_f16_out(const float *src, size_t n, uint16_t *dst, hipStream_t st);
 hipError_t read_and_clear_device_status(uint32_t *out);
 
 // Error reporting shared by the C-ABI sources: record `msg` (and a HIP

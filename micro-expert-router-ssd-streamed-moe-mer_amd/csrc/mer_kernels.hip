@@ -496,6 +496,30 @@ hipError_t launch_fill(int fmt, uint64_t seed, uint64_t expert, uint64_t block_b
   return hipSuccess;
 }
 
+// f16 <-> f32 staging of the f16-view entry point: x [d_model] repeated
+// n_rep times, and the outputs rounded to f16 (round to nearest even).
+__global__ __launch_bounds__(256) void f16_in_kernel(const _Float16 *x, size_t d_model, size_t n_rep, float *dst) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= d_model * n_rep) return;
+  dst[i] = (float)x[i % d_model];
+}
+__global__ __launch_bounds__(256) void f16_out_kernel(const float *src, size_t n, _Float16 *dst) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[i] = (_Float16)src[i];
+}
+
+hipError_t launch_f16_in(const uint16_t *x, size_t d_model, size_t n_rep, float *dst, hipStream_t st) {
+  const size_t n = d_model * n_rep;
+  hipLaunchKernelGGL(f16_in_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st,
+                     reinterpret_cast<const _Float16 *>(x), d_model, n_rep, dst);
+  return hipGetLastError();
+}
+hipError_t launch_f16_out(const float *src, size_t n, uint16_t *dst, hipStream_t st) {
+  hipLaunchKernelGGL(f16_out_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, src, n,
+                     reinterpret_cast<_Float16 *>(dst));
+  return hipGetLastError();
+}
+
 uint32_t *device_status_ptr() {
   void *ptr = nullptr;
   if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_device_status)) != hipSuccess) return nullptr;

@@ -187,6 +187,35 @@ def moe_forward(dtype: WeightDtype, d_model: int, d_ff: int, table: torch.Tensor
     return out
 
 
+def routed_expert_matmul_batch(dtype: WeightDtype, d_model: int, d_ff: int, table: torch.Tensor,
+                               expert_ids: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The GPU backend's f16-view batch: routed_expert_matmul_batch_q4
+    (backend/mod.rs:3770-3850, :4401-4418).  Every expert of expert_ids
+    (int32 [n]) runs on the same f16 hidden state x [d_model]; returns
+    f16 [n, d_model], row i = y of expert expert_ids[i] (not combined).
+    The reference takes exactly 8 experts; any n >= 1 is accepted here."""
+    _init_for(x)
+    n = expert_ids.numel()
+    if x.numel() != d_model:
+        raise ValueError("x must hold d_model elements")
+    if out is None:
+        out = torch.empty((n, d_model), dtype=torch.float16, device=x.device)
+    if out.numel() != n * d_model:
+        raise ValueError("out must hold n * d_model elements")
+    _call("mer_hip_expert_batch_f16", int(dtype), d_model, d_ff, n, *_table(table), _ptr(expert_ids, torch.int32),
+          _ptr(x, torch.float16), _ptr(out, torch.float16), _stream())
+    return out
+
+
+def expert_matmul(dtype: WeightDtype, d_model: int, d_ff: int, table: torch.Tensor, expert_id: int,
+                  x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Backend::expert_matmul / routed_expert_matmul (backend/mod.rs:1095-1103,
+    :4421-4441): one resident expert on an f16 hidden state, f16 [d_model] out."""
+    ids = torch.tensor([expert_id], dtype=torch.int32, device=x.device)
+    y = routed_expert_matmul_batch(dtype, d_model, d_ff, table, ids, x, None if out is None else out.view(1, d_model))
+    return y.view(d_model)
+
+
 def moe_grouped(dtype: WeightDtype, d_model: int, d_ff: int, table: torch.Tensor, expert_ids: torch.Tensor,
                 weights: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = None, *,
                 residual: bool = False, accumulate: bool = False) -> torch.Tensor:
