@@ -247,6 +247,50 @@ def run_cache_pressure(args, cfg, mer, routing, dev, stream):
     return result
 
 
+def router_pass(gates, xs_d, ids, L, E, K, dm, first_step, n_steps):
+    """The GPU LinearGate router (mer_hip_route_linear_gate, row a19) on the
+    config-2 steps' hidden states, one call per layer (logits kernel + select
+    kernel), all calls enqueued back to back between one pair of HIP events
+    on the current stream, so the figure is GPU time per call.  Reported
+    beside the expert path, not part of `value` (the timed steps route on the
+    host); `agreement` is the fraction of (step, layer) whose GPU top-k id set
+    equals the host routing's."""
+    import ctypes
+
+    import torch
+
+    mer = importlib.import_module(PKG)
+    dev = xs_d.device
+    lib = mer._lib.lib()
+    gates_d = torch.from_numpy(gates).to(dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    opts = mer._lib.MerGateOptions(0, 1, 0, 1, 1, 1.0)
+    calls = [(s, l) for s in range(first_step, first_step + n_steps) for l in range(L)]
+    ids_out = torch.empty((len(calls), K), dtype=torch.int32, device=dev)
+    w_out = torch.empty((len(calls), K), dtype=torch.float32, device=dev)
+    args = [(gates_d[l].data_ptr(), E, dm, xs_d[s, l].data_ptr(), 1, K, ctypes.byref(opts),
+             ids_out[i].data_ptr(), w_out[i].data_ptr(), None, stream) for i, (s, l) in enumerate(calls)]
+    fn = lib.mer_hip_route_linear_gate
+    for a in args[:L]:  # warm
+        fn(*a)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for a in args:
+        rc = fn(*a)
+        if rc:
+            mer.errors.raise_for_status(rc)
+    t1.record()
+    torch.cuda.synchronize()
+    avg = t0.elapsed_time(t1) * 1e3 / len(args)
+    got = ids_out.cpu().numpy()
+    agree = np.mean([set(got[i].tolist()) == set(ids[s, l, 0].tolist()) for i, (s, l) in enumerate(calls)])
+    nbytes = E * dm * 4 + dm * 4 + K * 8
+    return {"kernels": "router_logits_kernel + router_kernel", "calls": len(args), "avg_us_per_call": avg,
+            "bytes_per_call": nbytes, "gbps": nbytes / (avg * 1e-6) / 1e9,
+            "frac": nbytes / (avg * 1e-6) / 1e9 / HBM_PEAK_GBPS, "agreement": float(agree)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -529,6 +573,8 @@ def main() -> int:
                      "algorithmic_bytes_per_launch": stage_bytes[dominant], "avg_launch_us": dom["avg_us"]},
         "stages": stage_info,
     }
+    if args.config == 2:
+        result["router"] = router_pass(gates, xs_d, ids, L, E, K, dm, args.warmup, min(5, args.steps))
     traffic = read_traffic(args.config) if dominant == "decode" and not args.per_layer else None
     if traffic is not None:
         result["roofline"]["traffic"] = traffic["bytes"]

@@ -278,7 +278,9 @@ typedef struct mer_gate_options {
  *   finite score get id -1 and weight 0 (the routed forwards skip them);
  *   d_logits [n_tokens * n_experts] or NULL.
  * n_experts <= MER_MAX_ROUTER_EXPERTS, top_k <= MER_MAX_ROUTER_TOP_K,
- * d_model <= MER_MAX_EXPERT_DIM. */
+ * d_model <= MER_MAX_EXPERT_DIM, n_tokens <= 262144.  Without d_logits the
+ * library keeps the logits in a buffer of its own (grown on first use, so
+ * make one call of the largest shape before capturing a HIP graph). */
 int mer_hip_route_linear_gate(const float *d_gate, size_t n_experts, size_t d_model, const float *d_x,
                               size_t n_tokens, size_t top_k, const mer_gate_options *options, int32_t *d_ids,
                               float *d_weights, float *d_logits, void *stream);

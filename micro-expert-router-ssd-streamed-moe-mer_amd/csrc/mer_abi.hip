@@ -69,6 +69,8 @@ struct DeviceState {
   size_t scratch_floats = 0;
   float *stage = nullptr;        // f32 x and y of the f16-view entry point
   size_t stage_floats = 0;
+  float *router_buf = nullptr;   // router logits when the caller asks for none
+  size_t router_floats = 0;
   uint32_t *counters = nullptr;  // decode counters, all zero between launches
   size_t counter_words = 0;
   uint32_t *release = nullptr;   // decode release flags (epoch-valued, zero at allocation)
@@ -702,6 +704,7 @@ int mer_hip_shutdown(void) {
   (void)hipDeviceSynchronize();
   if (d.scratch) (void)hipFree(d.scratch);
   if (d.stage) (void)hipFree(d.stage);
+  if (d.router_buf) (void)hipFree(d.router_buf);
   if (d.counters) (void)hipFree(d.counters);
   if (d.release) (void)hipFree(d.release);
   d = DeviceState{};
@@ -1016,7 +1019,7 @@ int mer_hip_route_linear_gate(const float *d_gate, size_t n_experts, size_t d_mo
     return fail(MER_ERR_INVALID_LAYOUT, "top_k must be in 1..=min(n_experts, %u), got %zu", kMaxRouterTopK, top_k);
   if (d_model == 0 || d_model > MER_MAX_EXPERT_DIM)
     return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "router d_model must be in 1..=%d, got %zu", MER_MAX_EXPERT_DIM, d_model);
-  if (n_tokens > (1u << 30)) return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "too many tokens");
+  if (n_tokens > (1u << 18)) return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "the router takes at most 262144 tokens per call");
   RouterParams p{};
   p.gate = d_gate;
   p.x = d_x;
@@ -1043,6 +1046,27 @@ int mer_hip_route_linear_gate(const float *d_gate, size_t n_experts, size_t d_mo
     p.n_group = options->n_group;
     p.topk_group = options->topk_group;
     p.scaling = options->routed_scaling_factor;
+  }
+  p.logit_buf = d_logits;
+  if (!d_logits) {
+    DeviceState &d = g_dev[g_device];
+    const size_t need = n_tokens * n_experts;
+    if (d.router_floats < need) {
+      if (capturing((hipStream_t)stream))
+        return fail(MER_ERR_PHYSICAL_CAPACITY, "the router's logits buffer must grow, which cannot happen under graph "
+                                               "capture: run the same call once before capturing");
+      if (d.router_buf) {
+        hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) return hip_fail(e, MER_ERR_DEVICE_LOST, "synchronise before router buffer growth");
+        (void)hipFree(d.router_buf);
+        d.router_buf = nullptr;
+        d.router_floats = 0;
+      }
+      hipError_t e = hipMalloc(&d.router_buf, need * sizeof(float));
+      if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "router logits allocation");
+      d.router_floats = need;
+    }
+    p.logit_buf = d.router_buf;
   }
   hipError_t e = launch_router(p, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "router launch");

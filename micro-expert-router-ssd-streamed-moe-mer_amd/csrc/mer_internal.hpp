@@ -186,6 +186,7 @@ struct RouterParams {
   int32_t *ids;         // [n_tokens][top_k]; -1 where fewer experts qualify
   float *weights;       // [n_tokens][top_k]; 0 where fewer experts qualify
   float *logits;        // [n_tokens][n_experts], or null
+  float *logit_buf;     // [n_tokens][n_experts]: logits, or the library's buffer when logits is null
   uint32_t n_experts, d_model, n_tokens, top_k;
   int32_t scoring;      // 0 softmax, 1 sigmoid
   int32_t normalise;    // renormalise the top-k weights

@@ -61,22 +61,24 @@ def test_router_reference_known_answers(mer, gpu):
 
 
 ROUTER_CASES = [
-    # (n_experts, d_model, top_k, options)
-    (8, 64, 2, {}),
-    (128, 2048, 8, {}),
-    (256, 7168, 8, dict(sigmoid=True, bias=True, n_group=8, topk_group=4, scaling=2.5)),
-    (160, 1000, 6, dict(sigmoid=True, normalise=False)),
-    (1024, 512, 64, {}),
-    (64, 96, 4, dict(bias=True)),
+    # (n_experts, d_model, top_k, options, n_tokens); logits run in groups of 4 tokens,
+    # with 16-byte loads when d_model % 4 == 0 and scalar loads otherwise
+    (8, 64, 2, {}, 3),
+    (128, 2048, 8, {}, 3),
+    (128, 2048, 8, {}, 37),
+    (256, 7168, 8, dict(sigmoid=True, bias=True, n_group=8, topk_group=4, scaling=2.5), 3),
+    (160, 1000, 6, dict(sigmoid=True, normalise=False), 3),
+    (1024, 512, 64, {}, 3),
+    (64, 96, 4, dict(bias=True), 3),
+    (48, 99, 3, {}, 6),
 ]
 
 
-@pytest.mark.parametrize("n_experts,d_model,top_k,opts", ROUTER_CASES)
-def test_router_matches_oracle(mer, oracle, gpu, n_experts, d_model, top_k, opts):
-    say(f"router E={n_experts} dm={d_model} k={top_k} {opts}")
+@pytest.mark.parametrize("n_experts,d_model,top_k,opts,n_tok", ROUTER_CASES)
+def test_router_matches_oracle(mer, oracle, gpu, n_experts, d_model, top_k, opts, n_tok):
+    say(f"router E={n_experts} dm={d_model} k={top_k} {opts} tokens={n_tok}")
     r = routing(mer)
     rng = np.random.default_rng(n_experts * 31 + d_model)
-    n_tok = 3
     w = (rng.standard_normal((n_experts, d_model)) * 0.02).astype(np.float32)
     x = rng.standard_normal((n_tok, d_model)).astype(np.float32)
     o = dict(opts)
@@ -92,6 +94,23 @@ def test_router_matches_oracle(mer, oracle, gpu, n_experts, d_model, top_k, opts
         assert list(ids[t][:len(want_ids)]) == list(want_ids), f"ids token {t}"
         assert (ids[t][len(want_ids):] == -1).all()
         assert np.allclose(ws[t][:len(want_ws)], want_ws, rtol=1e-5, atol=1e-7), f"weights token {t}"
+
+
+def test_router_misaligned_input_takes_scalar_loads(mer, oracle, gpu):
+    """x one float past a 16-byte boundary (a valid contiguous view) routes
+    exactly as the aligned copy does, without logits requested."""
+    say("router misaligned x")
+    r = routing(mer)
+    rng = np.random.default_rng(3)
+    w = dev((rng.standard_normal((128, 2048)) * 0.02).astype(np.float32), gpu)
+    x = rng.standard_normal((5, 2048)).astype(np.float32)
+    flat = dev(np.concatenate([np.zeros(1, np.float32), x.ravel()]), gpu)
+    xm = flat[1:].view(5, 2048)
+    assert xm.data_ptr() % 16 != 0
+    ids_m, ws_m = r.route_linear_gate_gpu(w, xm, 8)
+    ids_a, ws_a = r.route_linear_gate_gpu(w, dev(x, gpu), 8)
+    assert torch.equal(ids_m, ids_a)
+    assert np.allclose(ws_m.cpu().numpy(), ws_a.cpu().numpy(), rtol=1e-5, atol=1e-7)
 
 
 def test_router_nonfinite_row_is_uniform(mer, gpu):
