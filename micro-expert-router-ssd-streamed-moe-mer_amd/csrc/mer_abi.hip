@@ -814,6 +814,7 @@ int mer_hip_q4_0_matvec(const void *d_weights, size_t weights_len, size_t w_bloc
     return fail(MER_ERR_INVALID_LAYOUT, "Q4_0 raw weights have %zu bytes, require at least %zu complete 18-byte blocks",
                 weights_len, required);
   if (rows > UINT32_MAX || bpr > UINT32_MAX) return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "raw matvec too large");
+  if (!d_weights || !d_input || !d_output) return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
   hipError_t e = launch_q4_raw((const uint8_t *)d_weights, w_block_off, (uint32_t)rows, (uint32_t)bpr, d_input,
                                d_output, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "raw matvec launch");
@@ -1079,6 +1080,8 @@ int mer_hip_fill_synthetic(int dtype, uint64_t seed, uint64_t expert_index, uint
   if (rc) return rc;
   if (dtype != MER_DTYPE_Q4_0 && dtype != MER_DTYPE_Q8_0)
     return fail(MER_ERR_UNSUPPORTED_DTYPE, "unsupported expert dtype %d", dtype);
+  if (n_blocks == 0) return MER_OK;
+  if (!d_dst) return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
   if (((uintptr_t)d_dst & 1u) != 0) return fail(MER_ERR_MISALIGNED, "fill destination must be 2-byte aligned");
   hipError_t e = launch_fill(fmt_of(dtype), seed, expert_index, block_begin, n_blocks, scale_lo, scale_hi,
                              (uint8_t *)d_dst, (hipStream_t)stream);

@@ -396,3 +396,30 @@ def test_moe_forward_layers_vs_oracle(mer, oracle, gpu, mode, dtype):
             assert_ffn_close(shared.cpu().numpy(), acc, f"launch {launch} accumulated")
     mer.take_device_status()
     del tables
+
+
+def test_null_device_pointers_rejected_before_launch(mer, gpu):
+    """Every entry point that takes device buffers refuses a null one with
+    MER_ERR_INVALID_LAYOUT before any kernel is launched."""
+    say("null device pointers")
+    lib = mer._lib.lib()
+    bad = mer._lib.Status.INVALID_LAYOUT
+    buf = torch.zeros(4096, dtype=torch.uint8, device=gpu)
+    f = torch.zeros(256, dtype=torch.float32, device=gpu)
+    assert lib.mer_hip_q4_0_matvec(None, 18, 0, 1, 32, f.data_ptr(), f.data_ptr(), None) == bad
+    assert lib.mer_hip_q4_0_matvec(buf.data_ptr(), 18, 0, 1, 32, None, f.data_ptr(), None) == bad
+    assert lib.mer_hip_q4_0_matvec(buf.data_ptr(), 18, 0, 1, 32, f.data_ptr(), None, None) == bad
+    assert lib.mer_hip_fill_synthetic(4, 1, 0, 0, 4, 0.01, 0.02, None, None) == bad
+    assert lib.mer_hip_fill_synthetic(4, 1, 0, 0, 0, 0.01, 0.02, None, None) == 0  # nothing to fill
+    assert lib.mer_hip_dequantize(4, None, 18, 32, f.data_ptr(), None) == bad
+    assert lib.mer_hip_expert_forward(4, None, 0, f.data_ptr(), 64, 64, 64, f.data_ptr(), 64, None) != 0
+    ids = torch.zeros((1, 1), dtype=torch.int32, device=gpu)
+    for args in ((None, 1, ids.data_ptr(), f.data_ptr(), f.data_ptr(), f.data_ptr()),
+                 (buf.data_ptr(), 1, None, f.data_ptr(), f.data_ptr(), f.data_ptr()),
+                 (buf.data_ptr(), 1, ids.data_ptr(), f.data_ptr(), None, f.data_ptr())):
+        table, n, i, w, x, o = args
+        assert lib.mer_hip_moe_forward(4, 64, 64, 1, 1, table, n, i, w, x, o, 0, None) == bad
+        assert lib.mer_hip_moe_grouped(4, 64, 64, 1, 1, table, n, i, w, x, o, 0, None) == bad
+    assert lib.mer_hip_expert_batch_f16(4, 64, 64, 1, buf.data_ptr(), 1, ids.data_ptr(), None, f.data_ptr(), None) == bad
+    torch.cuda.synchronize()
+    mer.take_device_status()
