@@ -86,6 +86,14 @@ __device__ __forceinline__ void set_status(const DecodeParams &p, uint32_t code)
   atomicCAS(p.status, 0u, code);
 }
 
+// Wave priority on the SIMD.  A wave runs its hand-off work (digit
+// fetches, arrivals, combines, packing) at raised priority, so the
+// instructions on the layer's critical path issue ahead of the weight walks
+// of the other waves sharing its SIMD (measured, Mixtral decode: 708 -> 720
+// tokens/s; raising the prefetch issue or the walk itself gains nothing).
+__device__ __forceinline__ void prio_hi() { __builtin_amdgcn_s_setprio(2); }
+__device__ __forceinline__ void prio_lo() { __builtin_amdgcn_s_setprio(0); }
+
 constexpr uint32_t kNapCounter = 16;  // longest nap between polls of a shared counter, in ~0.05 us
 constexpr uint32_t kNapFlag = 2;      // ... of a release flag
 
@@ -495,7 +503,9 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       tm.ready = trace_now(p);
       uint32_t xd[2 * kBlockDigitDwords];
       float xsc[2];
+      prio_hi();
       fetch_digits(xq_dig, (size_t)t * p.xblocks + 2 * (size_t)c, valid, p.epoch, xd, xsc);
+      prio_lo();
       tm.fetched = trace_now(p);
       float *gpart = p.gpart + (((size_t)l * p.n_inst + inst) * p.g_slices + gs) * 2 * p.d_ff;
       const bool single_slice = p.g_slices == 1;
@@ -510,6 +520,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
         }
       };
       walk.run(wbuf, xd, xsc, emit);
+      prio_hi();
       tm.walked = trace_now(p);
       bool pack = single_slice;
       if (!single_slice) {
@@ -568,7 +579,9 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       tm.ready = trace_now(p);
       uint32_t xd[2 * kBlockDigitDwords];
       float xsc[2];
+      prio_hi();
       fetch_digits(hq_dig, (size_t)inst * p.hblocks + 2 * (size_t)c, valid, p.epoch, xd, xsc);
+      prio_lo();
       tm.fetched = trace_now(p);
       float *part = p.partial + (((size_t)l * p.n_inst + inst) * p.d_slices + ds) * p.d_model;
       // Row sums go to LDS, then out as one 128-byte store.  The slot weight
@@ -579,6 +592,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
         if (gl == 0) s_h[r - tile * kTileRows] = a[0];
       };
       walk.run(wbuf, xd, xsc, emit);
+      prio_hi();
       tm.walked = trace_now(p);
       __syncthreads();
       // What a combine of this tile adds to the sum is already final: the
@@ -637,6 +651,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       }
     }
     trace_item(p, gi, tm);
+    prio_lo();
   }
 
   // the last wave out zeroes the counters for the next launch
