@@ -313,7 +313,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(experts would shard id % n_gpu; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(experts would shard by id % n_gpu across GPUs). Run with --gpus 1.", file=sys.stderr)
         return 2
 
     import torch
