@@ -13,7 +13,8 @@
 // Launches, all on the caller's stream:
 //   group_kernel   block 0 groups the routed pairs by expert (counting
 //                  sort) and emits token tiles of <= 16 pairs per expert;
-//                  the other blocks quantise x into 16-bit digit pairs
+//                  the other blocks quantise x into 24-bit digit records
+//                  (three base-256 planes, below)
 //   proj_kernel<FUSED>  one workgroup per (token tile, 32 rows of d_ff):
 //                  gate and up rows for the tile's tokens, SiLU * up, h
 //                  quantised per 32-element block
@@ -51,7 +52,14 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kGTok = 16;           // pairs per token tile (MFMA N)
 constexpr uint32_t kGRows = 64;          // weight rows staged per workgroup
-constexpr uint32_t kGStageBlocks = 16;   // K blocks per LDS stage
+// K blocks per LDS stage.  Eight-block stages with two in flight per
+// workgroup (one two-block chunk per thread and stage) beat sixteen-block
+// stages with one in flight (measured on the 64-token Qwen3 batch: down
+// 39 -> 36 us, 493K -> 508K tokens/s; gate/up unchanged).
+constexpr uint32_t kGStageBlocks = 8;
+constexpr uint32_t kGStageChunks = kGStageBlocks / 2;  // two-block chunks per row per stage
+constexpr int kGChunksPerThread = (int)(kGRows * kGStageChunks / 256);
+constexpr int kGWaveBlocks = (int)(kGStageBlocks / 4);  // blocks of a stage per wave
 constexpr uint32_t kGRowStride = kGStageBlocks * 32 + 16;  // LDS bytes per staged row
 // Scales are stored [block][row] with a padded row of 68 floats: the eight
 // threads that stage one row's chunks write 8 different banks.
@@ -206,17 +214,18 @@ __global__ __launch_bounds__(1024) void group_kernel(GroupedParams p) {
     if (pos[q] != 0xffffffffu) p.plist[cnt[p.ids[q]] + pos[q]] = q;
 }
 
-// Stage one 64-row x 16-block slab of weights into LDS: 512 two-block
-// chunks, two per thread, loaded with raw buffer loads (a chunk past the
-// row's end reads zeros) and stored as int8 rows plus f32 scales.
+// Stage one 64-row x kGStageBlocks-block slab of weights into LDS: two-block
+// chunks, kGChunksPerThread per thread, loaded with raw buffer loads into a
+// register buffer (a chunk past the row's end reads zeros) and stored as
+// int8 rows plus f32 scales.
 template <int FMT>
 struct Stager {
   using T = FmtTraits<FMT>;
   static constexpr int kDw = T::kChunkDwords;
   __amdgpu_buffer_rsrc_t rsrc[2];
-  uint32_t voff[2];      // byte offset of this thread's chunk c (stage 0), or kNoChunkG
-  uint32_t srow[2], schunk[2];
-  uint32_t w[2][kDw];
+  uint32_t voff[kGChunksPerThread];      // byte offset of this thread's chunk c (stage 0), or kNoChunkG
+  uint32_t srow[kGChunksPerThread], schunk[kGChunksPerThread];
+  using Buf = uint32_t[kGChunksPerThread][kDw];
 
   // fused: slab rows 0..31 come from base0 (gate), rows 32..63 from base1
   // (up), both starting at row 0; otherwise all 64 rows from base0.
@@ -224,22 +233,22 @@ struct Stager {
     rsrc[0] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base0), 0, 0x7fffffff, 0x00020000);
     rsrc[1] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base1), 0, 0x7fffffff, 0x00020000);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t c = threadIdx.x + 256u * i;  // chunk of the slab: row c / 8, chunk c % 8
-      srow[i] = c / 8;
-      schunk[i] = c % 8;
+    for (int i = 0; i < kGChunksPerThread; ++i) {
+      const uint32_t c = threadIdx.x + 256u * i;  // chunk of the slab: row c / kGStageChunks
+      srow[i] = c / kGStageChunks;
+      schunk[i] = c % kGStageChunks;
       const uint32_t r = fused ? srow[i] % 32 : srow[i];
       voff[i] = r * row_bytes + schunk[i] * (uint32_t)T::kChunkBytes;
     }
   }
 
-  // Issue the loads of stage s (chunks s*8 .. s*8+7 of each row).
-  __device__ __forceinline__ void load(uint32_t s, uint32_t row_chunks, bool fused) {
+  // Issue the loads of stage s (its kGStageChunks chunks of each row) into w.
+  __device__ __forceinline__ void load(uint32_t s, uint32_t row_chunks, bool fused, Buf &w) const {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kGChunksPerThread; ++i) {
       const int which = fused && srow[i] >= 32 ? 1 : 0;
-      const bool ok = s * 8 + schunk[i] < row_chunks;
-      const uint32_t off = ok ? voff[i] + s * 8u * (uint32_t)T::kChunkBytes : kNoChunkG;
+      const bool ok = s * kGStageChunks + schunk[i] < row_chunks;
+      const uint32_t off = ok ? voff[i] + s * kGStageChunks * (uint32_t)T::kChunkBytes : kNoChunkG;
 #pragma unroll
       for (int v = 0; v < kDw / 4; ++v) {
         const uint4 q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc[which], off + 16 * v, 0, 0));
@@ -254,9 +263,9 @@ struct Stager {
 
   // Write the loaded chunks to LDS: q as int8 [row][block][32], scales
   // as f32 [block][row].
-  __device__ __forceinline__ void store(uint8_t *lq, float *ld) const {
+  __device__ __forceinline__ void store(const Buf &w, uint8_t *lq, float *ld) const {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kGChunksPerThread; ++i) {
       uint32_t q0[8], q1[8];
       float d0, d1;
       if constexpr (FMT == FMT_Q4_0) {
@@ -324,7 +333,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
     const uint8_t *d = gt.blob + 2 * p.proj_bytes + (size_t)rt * kGRows * row_bytes;
     sg.init(d, d, row_bytes, false);
   }
-  sg.load(0, row_chunks, FUSED);
+  const uint32_t n_stages = (kblocks + kGStageBlocks - 1) / kGStageBlocks;
+  // Two stages in flight: stage s + 2 loads into the buffer stage s leaves.
+  typename Stager<FMT>::Buf wbuf[2];
+  sg.load(0, row_chunks, FUSED, wbuf[0]);
+  if (n_stages > 1) sg.load(1, row_chunks, FUSED, wbuf[1]);
   __syncthreads();  // s_pair
 
   // B operands: the lane's column is pair s_pair[lane % 16]; its k-group is lane / 16
@@ -349,16 +362,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[a][i] = 0.f;
 
-  const uint32_t n_stages = (kblocks + kGStageBlocks - 1) / kGStageBlocks;
-  // B operands of this wave's blocks of stage s (wave, wave + 4, wave + 8,
-  // wave + 12), loaded one stage ahead: the loads of stage s + 1 are issued
-  // right after stage s's MFMAs, so they arrive during the slab store.
-  uint2 bv[4][3];
-  float bs[4];
+  // B operands of this wave's blocks of stage s (wave, wave + 4, ...),
+  // loaded one stage ahead: the loads of stage s + 1 are issued right after
+  // stage s's MFMAs, so they arrive during the slab store.
+  uint2 bv[kGWaveBlocks][3];
+  float bs[kGWaveBlocks];
   auto load_b = [&](uint32_t s) {
     const uint32_t nb = min(kGStageBlocks, kblocks - s * kGStageBlocks);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kGWaveBlocks; ++j) {
       const uint32_t b = wave + 4 * j;
       const bool ok = col_ok && b < nb;
       const uint32_t gb = s * kGStageBlocks + b;
@@ -368,13 +380,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
     }
   };
   load_b(0);
-  for (uint32_t s = 0; s < n_stages; ++s) {
-    sg.store(lq, ld);
+  auto stage = [&](uint32_t s, typename Stager<FMT>::Buf &w) {
+    sg.store(w, lq, ld);
     __syncthreads();
-    if (s + 1 < n_stages) sg.load(s + 1, row_chunks, FUSED);
+    if (s + 2 < n_stages) sg.load(s + 2, row_chunks, FUSED, w);
     const uint32_t nb = min(kGStageBlocks, kblocks - s * kGStageBlocks);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kGWaveBlocks; ++j) {
       const uint32_t b = wave + 4 * j;
       if (b >= nb) break;  // uniform
       long bk[3];
@@ -399,6 +411,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
     }
     if (s + 1 < n_stages) load_b(s + 1);
     __syncthreads();  // LDS slab consumed before the next store
+  };
+  for (uint32_t s = 0; s < n_stages; s += 2) {
+    stage(s, wbuf[0]);
+    if (s + 1 < n_stages) stage(s + 1, wbuf[1]);
   }
 
   // sum the four waves' partials (in the slab's LDS, free now); wave w
