@@ -478,15 +478,27 @@ __global__ __launch_bounds__(256) void gcombine_kernel(GroupedParams p) {
   const uint32_t per_tok = p.d_model / 4;
   if (q >= p.n_tok * per_tok) return;
   const uint32_t t = q / per_tok, c = (q % per_tok) * 4;
+  // Slots are summed in slot order; the loads of up to eight slots are
+  // issued before any is used, so the combine costs one memory round trip
+  // per eight slots instead of one per slot.
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (uint32_t k = 0; k < p.top_k; ++k) {
-    const uint32_t pr = t * p.top_k + k;
-    if (!p.pair_ok[pr]) continue;
-    const float4 v = *reinterpret_cast<const float4 *>(p.partial + (size_t)pr * p.d_model + c);
-    acc.x += v.x;
-    acc.y += v.y;
-    acc.z += v.z;
-    acc.w += v.w;
+  for (uint32_t k0 = 0; k0 < p.top_k; k0 += 8) {
+    bool ok[8];
+    float4 v[8];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) ok[j] = k0 + j < p.top_k && p.pair_ok[t * p.top_k + k0 + j];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j)
+      v[j] = ok[j] ? *reinterpret_cast<const float4 *>(p.partial + (size_t)(t * p.top_k + k0 + j) * p.d_model + c)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j)
+      if (ok[j]) {
+        acc.x += v[j].x;
+        acc.y += v[j].y;
+        acc.z += v[j].z;
+        acc.w += v[j].w;
+      }
   }
   float4 *o = reinterpret_cast<float4 *>(p.out + (size_t)t * p.d_model + c);
   if (p.flags & (kFlagResidual | kFlagAccumulate)) {
