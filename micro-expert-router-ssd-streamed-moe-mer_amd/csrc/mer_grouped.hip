@@ -61,8 +61,8 @@ constexpr uint32_t kGStageChunks = kGStageBlocks / 2;  // two-block chunks per r
 constexpr int kGChunksPerThread = (int)(kGRows * kGStageChunks / 256);
 constexpr int kGWaveBlocks = (int)(kGStageBlocks / 4);  // blocks of a stage per wave
 constexpr uint32_t kGRowStride = kGStageBlocks * 32 + 16;  // LDS bytes per staged row
-// Scales are stored [block][row] with a padded row of 68 floats: the eight
-// threads that stage one row's chunks write 8 different banks.
+// Scales are stored [block][row] with a padded row of 68 floats, so the
+// threads that stage consecutive rows' chunks write different banks.
 constexpr uint32_t kGScaleStride = kGRows + 4;
 constexpr float kGIntMax = 8355711.0f;   // |v| bound (0x7f7f7f): v + 0x808080 stays in 24 bits
 constexpr uint32_t kGRec = 6;            // dwords per (vector, block, k-group) digit record
