@@ -178,21 +178,33 @@ __global__ __launch_bounds__(1024) void group_kernel(GroupedParams p) {
     sp += c;
     st += (c + kGTok - 1) / kGTok;
   }
-  part[tid] = sp;
-  part[nth + tid] = st;
-  __syncthreads();
-  for (uint32_t off = 1; off < nth; off <<= 1) {  // Hillis-Steele inclusive scan
-    uint32_t a = 0, b = 0;
-    if (tid >= off) {
-      a = part[tid - off];
-      b = part[nth + tid - off];
+  // Inclusive scan of (sp, st) over the block: within each wave by lane
+  // shuffles, then over the wave totals (two barriers in all).
+  uint32_t ip = sp, it = st;
+  for (uint32_t off = 1; off < 64; off <<= 1) {
+    const uint32_t a = __shfl_up(ip, off, 64), b = __shfl_up(it, off, 64);
+    if (lane_id() >= off) {
+      ip += a;
+      it += b;
     }
-    __syncthreads();
-    part[tid] += a;
-    part[nth + tid] += b;
-    __syncthreads();
   }
-  uint32_t op = part[tid] - sp, ot = part[nth + tid] - st;
+  const uint32_t wave = tid / 64, n_waves = (nth + 63) / 64;
+  if (lane_id() == 63) {
+    part[wave] = ip;
+    part[nth + wave] = it;
+  }
+  __syncthreads();
+  if (tid == 0)
+    for (uint32_t w = 1; w < n_waves; ++w) {
+      part[w] += part[w - 1];
+      part[nth + w] += part[nth + w - 1];
+    }
+  __syncthreads();
+  if (wave > 0) {
+    ip += part[wave - 1];
+    it += part[nth + wave - 1];
+  }
+  uint32_t op = ip - sp, ot = it - st;
   for (uint32_t e = e0; e < e1; ++e) {
     const uint32_t c = cnt[e];
     const uint32_t nt = (c + kGTok - 1) / kGTok;
@@ -208,7 +220,7 @@ __global__ __launch_bounds__(1024) void group_kernel(GroupedParams p) {
     op += c;
     ot += nt;
   }
-  if (tid == nth - 1) *p.n_tiles = part[nth + tid];
+  if (tid == nth - 1) *p.n_tiles = it;
   __syncthreads();
   for (uint32_t q = tid; q < p.n_pairs; q += nth)
     if (pos[q] != 0xffffffffu) p.plist[cnt[p.ids[q]] + pos[q]] = q;
