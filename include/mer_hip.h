@@ -19,11 +19,24 @@
  *     each projection an independently block-rounded stream of GGUF
  *     blocks (inference.rs:1089-1146); gate/up are [d_ff x d_model] and
  *     down is [d_model x d_ff], row-major.
- *   - Re-entrant: calls on different streams may run concurrently; calls
- *     that share the library's per-device scratch (mer_hip_expert_forward,
- *     mer_hip_moe_forward) are serialised onto the caller's stream order,
- *     so concurrent use needs one stream per caller thread and the
- *     caller must not overlap two such calls on different streams.
+ *   - Re-entrant.  Each stream has a workspace of its own (scratch,
+ *     decode counters and flags, staging), created on the first call that
+ *     uses the stream, so calls on different streams never share device
+ *     state and may run concurrently from any host threads (the engine's
+ *     parallel expert workers, or several concurrent dispatches, each
+ *     with its own stream: backend/mod.rs:1346-1432, :2685-2697).  Calls
+ *     on one stream from several threads are serialised by the stream's
+ *     workspace lock and run in stream order.  The persistent decode
+ *     kernel claims its work items in order from a counter, so it
+ *     completes whatever else runs on the device (it needs no
+ *     co-residency of its grid).  Release a stream's workspace with
+ *     mer_hip_stream_release before destroying the stream.
+ *   - Graph capture: every device entry point may be captured into a HIP
+ *     graph once a call of the same shape has run on that stream (the
+ *     workspace grows only outside capture; growth under capture fails
+ *     with MER_ERR_PHYSICAL_CAPACITY).  Replays are correct: the decode
+ *     kernel's epoch lives in device memory and each launch hands the
+ *     next one a fresh value.
  */
 #ifndef MER_HIP_H
 #define MER_HIP_H
@@ -93,6 +106,11 @@ int mer_hip_abi_version(void);
  * (backend/mod.rs:2202-2260). */
 int mer_hip_init(int device);
 int mer_hip_shutdown(void);
+/* Free the workspace of `stream` (synchronises that stream).  Call it
+ * before destroying a stream the library has used; the next call on the
+ * stream creates a new workspace.  No reference counterpart (the
+ * reference's dispatch workspaces live as long as their backend). */
+int mer_hip_stream_release(void *stream);
 const char *mer_last_error(void);
 int mer_last_error_info(mer_error_info *out);
 /* Device fault word written by kernels (bad expert id, null table entry):
@@ -246,8 +264,9 @@ typedef struct mer_layer_args {
  * (layer l starts reading its input only after layer l-1 has written its
  * output), with the same combine order and flags as mer_hip_moe_forward;
  * under MER_MOE_CHAIN layer l's input is layer l-1's out.  Requires
- * d_model and d_ff to be multiples of 64.  The launch occupies every CU;
- * run nothing else on the device concurrently. */
+ * d_model and d_ff to be multiples of 64.  The launch sizes its grid to
+ * fill every CU; other work on the device (other streams) shares the CUs
+ * and slows it, but cannot stall it (items are claimed in order). */
 int mer_hip_moe_forward_layers(int dtype, size_t d_model, size_t d_ff, size_t n_layers, size_t n_tokens,
                                size_t top_k, const mer_layer_args *layers, unsigned flags, void *stream);
 

@@ -43,6 +43,7 @@ from .expert import (
     routed_expert_matmul_batch,
     stage_timing_enable,
     stage_timing_read,
+    stream_release,
     take_device_status,
     validate_expert,
 )

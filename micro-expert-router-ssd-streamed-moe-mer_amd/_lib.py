@@ -102,6 +102,7 @@ SIGNATURES = {
     "mer_hip_abi_version": (c_int, []),
     "mer_hip_init": (c_int, [c_int]),
     "mer_hip_shutdown": (c_int, []),
+    "mer_hip_stream_release": (c_int, [c_void]),
     "mer_last_error": (ctypes.c_char_p, []),
     "mer_last_error_info": (c_int, [ctypes.POINTER(MerErrorInfo)]),
     "mer_hip_take_device_status": (c_int, []),

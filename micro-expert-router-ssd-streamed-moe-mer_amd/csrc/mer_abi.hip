@@ -6,8 +6,11 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
+#include <memory>
 #include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "../../include/mer_hip.h"
@@ -62,29 +65,65 @@ size_t div_ceil(size_t a, size_t b) { return a / b + (a % b != 0); }
 size_t block_bytes(int dtype) { return dtype == MER_DTYPE_Q4_0 ? 18 : 34; }
 int fmt_of(int dtype) { return dtype == MER_DTYPE_Q4_0 ? FMT_Q4_0 : FMT_Q8_0; }
 
-struct DeviceState {
-  bool ready = false;
-  int cus = 256;
-  float *scratch = nullptr;
+// Per-stream workspace.  Everything a device entry point writes besides
+// its outputs (scratch, decode counters, release flags, staging) belongs to
+// the workspace of the caller's stream, so calls on different streams never
+// share device state and may run concurrently, from any host threads.  The
+// workspace's mutex is held for the whole host part of a call (validation
+// aside), so calls on one stream from several threads are serialised on the
+// host and ordered on the device by the stream.
+struct Workspace {
+  std::mutex mu;
+  hipStream_t stream = nullptr;
+  float *scratch = nullptr;      // h vectors, digit lines, partial sums
   size_t scratch_floats = 0;
   float *stage = nullptr;        // f32 x and y of the f16-view entry point
   size_t stage_floats = 0;
   float *router_buf = nullptr;   // router logits when the caller asks for none
   size_t router_floats = 0;
-  uint32_t *counters = nullptr;  // decode counters, all zero between launches
+  uint32_t *counters = nullptr;  // decode counters (zero between launches) + control lines
   size_t counter_words = 0;
-  uint32_t *release = nullptr;   // decode release flags (epoch-valued, zero at allocation)
+  uint64_t *release = nullptr;   // decode release flags (epoch-valued, zero at allocation)
   size_t release_words = 0;
+};
+
+// Control lines at the end of a workspace's counter allocation, one
+// 256-byte line each: exit count, abort flag, launch epoch.
+constexpr size_t kCtlLines = 3;
+
+struct DeviceState {
+  bool ready = false;
+  int cus = 256;
   uint32_t *status = nullptr;
   uint64_t clock_khz = 100000;
-  uint64_t *trace = nullptr;     // decode item trace buffer (caller-owned)
-  uint64_t trace_cap = 0;
-  uint32_t decode_epoch = 0;     // launches of the decode kernel so far
-  int occupancy[2][3][3] = {};   // resident decode workgroups per CU, by (fmt, GG, GD)
+  std::atomic<int> occupancy[2][3][3] = {};  // resident decode workgroups per CU, by (fmt, GG, GD)
+  // The first stream to launch the persistent decode kernel on this device.
+  // Its launches are plain; every other stream's are cooperative.  Plain
+  // launches (one stream, so one at a time) wait, if other kernels hold CUs,
+  // only until those kernels finish; cooperative grids are resident whole.
+  // So no two partly resident persistent grids can ever wait on each other,
+  // and a single engine stream does not pay the cooperative launch's extra
+  // ~16 us per launch.
+  std::atomic<uintptr_t> primary_stream{UINTPTR_MAX};
+  std::unordered_map<hipStream_t, std::unique_ptr<Workspace>> ws;  // guarded by g_mu
 };
+// Lock order: g_mu, then a workspace's mutex.  Code holding a workspace's
+// mutex takes only the leaf locks (g_timing_mu, g_trace_mu, g_launch_mu),
+// never g_mu.
 std::mutex g_mu;
-int g_device = -1;
+std::atomic<int> g_device{-1};
 DeviceState g_dev[64];
+// First epochs of new counter allocations (below 2^63; the kernels hand out
+// epochs with bit 63 set), so no two workspaces ever share an epoch.
+std::atomic<uint64_t> g_host_epoch{0};
+
+// Serialises the enqueueing of decode launches (a leaf lock).
+std::mutex g_launch_mu;
+
+// Decode item trace (tracing aid), a leaf lock.
+std::mutex g_trace_mu;
+uint64_t *g_trace = nullptr;
+uint64_t g_trace_cap = 0;
 
 // GPU stage timings (stage_timing.rs:6-29 analogue): when enabled, every
 // gate/up, down and combine launch is bracketed by a pair of events on the
@@ -94,36 +133,40 @@ struct TimedLaunch {
   hipEvent_t start, end;
   int stage;
 };
-bool g_timing = false;
+std::mutex g_timing_mu;  // leaf lock: guards g_timed / g_timed_used
+std::atomic<bool> g_timing{false};
 std::vector<TimedLaunch> g_timed;
 size_t g_timed_used = 0;
 
-int timing_begin(int stage, hipStream_t st, TimedLaunch **slot) {
-  *slot = nullptr;
-  if (!g_timing) return MER_OK;
+int timing_begin(int stage, hipStream_t st, size_t *slot) {
+  *slot = SIZE_MAX;
+  if (!g_timing.load()) return MER_OK;
+  std::lock_guard<std::mutex> lk(g_timing_mu);
   if (g_timed_used == g_timed.size()) {
     TimedLaunch t{};
     if (hipEventCreate(&t.start) != hipSuccess || hipEventCreate(&t.end) != hipSuccess)
       return fail(MER_ERR_RUNTIME_INVARIANT, "stage timing event creation failed");
     g_timed.push_back(t);
   }
-  TimedLaunch *t = &g_timed[g_timed_used++];
-  t->stage = stage;
-  hipError_t e = hipEventRecord(t->start, st);
+  const size_t i = g_timed_used++;
+  g_timed[i].stage = stage;
+  hipError_t e = hipEventRecord(g_timed[i].start, st);
   if (e != hipSuccess) return fail(MER_ERR_SUBMISSION, "stage timing record: %s", hipGetErrorString(e));
-  *slot = t;
+  *slot = i;
   return MER_OK;
 }
 
-int timing_end(TimedLaunch *t, hipStream_t st) {
-  if (!t) return MER_OK;
-  hipError_t e = hipEventRecord(t->end, st);
+int timing_end(size_t slot, hipStream_t st) {
+  if (slot == SIZE_MAX) return MER_OK;
+  std::lock_guard<std::mutex> lk(g_timing_mu);
+  if (slot >= g_timed_used) return MER_OK;  // timings were read meanwhile
+  hipError_t e = hipEventRecord(g_timed[slot].end, st);
   if (e != hipSuccess) return fail(MER_ERR_SUBMISSION, "stage timing record: %s", hipGetErrorString(e));
   return MER_OK;
 }
 
 int require_init() {
-  if (g_device < 0) return fail(MER_ERR_NOT_INITIALIZED, "mer_hip_init has not been called");
+  if (g_device.load() < 0) return fail(MER_ERR_NOT_INITIALIZED, "mer_hip_init has not been called");
   return MER_OK;
 }
 
@@ -131,24 +174,30 @@ int hip_fail(hipError_t e, int status, const char *what) {
   return fail(status, "%s: %s", what, hipGetErrorString(e));
 }
 
-// Grow the per-device scratch (h vectors and down-projection partials).
-int ensure_scratch(size_t floats, float **out) {
-  DeviceState &d = g_dev[g_device];
-  if (d.scratch_floats < floats) {
-    if (d.scratch) {
-      hipError_t e = hipDeviceSynchronize();
-      if (e != hipSuccess) return hip_fail(e, MER_ERR_DEVICE_LOST, "synchronise before scratch growth");
-      (void)hipFree(d.scratch);
-      d.scratch = nullptr;
-      d.scratch_floats = 0;
-    }
-    size_t want = floats < (1u << 20) ? (1u << 20) : floats;
-    hipError_t e = hipMalloc(&d.scratch, want * sizeof(float));
-    if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "scratch allocation");
-    d.scratch_floats = want;
+// The workspace of `st` on the current device, created on first use.
+Workspace *workspace_for(hipStream_t st) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  const int dv = g_device.load();
+  if (dv < 0) return nullptr;
+  auto &slot = g_dev[dv].ws[st];
+  if (!slot) {
+    slot.reset(new Workspace());
+    slot->stream = st;
   }
-  *out = d.scratch;
-  return MER_OK;
+  return slot.get();
+}
+
+void free_workspace(Workspace &w) {
+  (void)hipStreamSynchronize(w.stream);
+  if (w.scratch) (void)hipFree(w.scratch);
+  if (w.stage) (void)hipFree(w.stage);
+  if (w.router_buf) (void)hipFree(w.router_buf);
+  if (w.counters) (void)hipFree(w.counters);
+  if (w.release) (void)hipFree(w.release);
+  w.scratch = w.stage = w.router_buf = nullptr;
+  w.counters = nullptr;
+  w.release = nullptr;
+  w.scratch_floats = w.stage_floats = w.router_floats = w.counter_words = w.release_words = 0;
 }
 
 bool capturing(hipStream_t st) {
@@ -156,57 +205,68 @@ bool capturing(hipStream_t st) {
   return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
 }
 
-// Decode counters live in their own allocation so they stay zero whatever
-// layout the scratch takes (the kernel re-zeroes what it used on exit).
-int ensure_counters(size_t words, hipStream_t st, uint32_t **out) {
-  DeviceState &d = g_dev[g_device];
-  words += 2 * kPollStride;  // + abort flag and exit counter, a line each
-  if (d.counter_words < words) {
-    if (capturing(st))
-      return fail(MER_ERR_PHYSICAL_CAPACITY, "decode counters must grow, which cannot happen under graph capture: "
-                                             "run the same call once before capturing");
-    if (d.counters) {
-      hipError_t e = hipDeviceSynchronize();
-      if (e != hipSuccess) return hip_fail(e, MER_ERR_DEVICE_LOST, "synchronise before counter growth");
-      (void)hipFree(d.counters);
-      d.counters = nullptr;
-      d.counter_words = 0;
-    }
-    size_t want = words < (1u << 16) ? (1u << 16) : words;
-    hipError_t e = hipMalloc(&d.counters, want * 4);
-    if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "decode counter allocation");
-    e = hipMemset(d.counters, 0, want * 4);
-    if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "decode counter initialisation");
-    d.counter_words = want;
+// Grow one of a workspace's buffers to at least `need` elements (at least
+// `min_elems`).  The old buffer is freed after the workspace's stream has
+// drained (the only stream that uses it).  With `zero`, the new buffer is
+// cleared on that stream.
+template <class T>
+int ensure_buf(Workspace &w, T **buf, size_t *cap, size_t need, size_t min_elems, bool zero, const char *what) {
+  if (*cap >= need) return MER_OK;
+  if (capturing(w.stream))
+    return fail(MER_ERR_PHYSICAL_CAPACITY,
+                "%s must grow, which cannot happen under graph capture: run the same call once before capturing", what);
+  if (*buf) {
+    hipError_t e = hipStreamSynchronize(w.stream);
+    if (e != hipSuccess) return hip_fail(e, MER_ERR_DEVICE_LOST, "synchronise before workspace growth");
+    (void)hipFree(*buf);
+    *buf = nullptr;
+    *cap = 0;
   }
-  *out = d.counters;
+  const size_t want = need < min_elems ? min_elems : need;
+  hipError_t e = hipMalloc(reinterpret_cast<void **>(buf), want * sizeof(T));
+  if (e != hipSuccess) {
+    *buf = nullptr;
+    return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, what);
+  }
+  if (zero) {
+    e = hipMemsetAsync(*buf, 0, want * sizeof(T), w.stream);
+    if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, what);
+  }
+  *cap = want;
   return MER_OK;
 }
 
-// Release flags: zeroed once when (re)allocated, never cleared by kernels
-// (they hold launch epochs, and every launch has a newer one).
-int ensure_release(size_t words, hipStream_t st, uint32_t **out) {
-  DeviceState &d = g_dev[g_device];
-  if (d.release_words < words) {
-    if (capturing(st))
-      return fail(MER_ERR_PHYSICAL_CAPACITY, "decode release flags must grow, which cannot happen under graph capture: "
-                                             "run the same call once before capturing");
-    if (d.release) {
-      hipError_t e = hipDeviceSynchronize();
-      if (e != hipSuccess) return hip_fail(e, MER_ERR_DEVICE_LOST, "synchronise before release-flag growth");
-      (void)hipFree(d.release);
-      d.release = nullptr;
-      d.release_words = 0;
-    }
-    size_t want = words < (1u << 16) ? (1u << 16) : words;
-    hipError_t e = hipMalloc(&d.release, want * 4);
-    if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "decode release-flag allocation");
-    e = hipMemset(d.release, 0, want * 4);
-    if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "decode release-flag initialisation");
-    d.release_words = want;
+int ensure_scratch(Workspace &w, size_t floats, float **out) {
+  int rc = ensure_buf(w, &w.scratch, &w.scratch_floats, floats, size_t(1) << 20, false, "scratch allocation");
+  *out = w.scratch;
+  return rc;
+}
+
+// Decode counters: `words` per launch plus the control lines, all zero
+// between launches (the kernel re-zeroes what it used on exit), except the
+// epoch word, which is given a first epoch unique in this process.
+int ensure_counters(Workspace &w, size_t words, uint32_t **out) {
+  words += kCtlLines * kPollStride;
+  const bool grow = w.counter_words < words;
+  int rc = ensure_buf(w, &w.counters, &w.counter_words, words, size_t(1) << 16, true, "decode counter allocation");
+  if (rc) return rc;
+  if (grow) {
+    const uint64_t first = ++g_host_epoch;
+    uint32_t *ctl = w.counters + w.counter_words - kCtlLines * kPollStride;
+    hipError_t e = hipMemcpyAsync(ctl + 2 * kPollStride, &first, sizeof first, hipMemcpyHostToDevice, w.stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(w.stream);
+    if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "decode counter initialisation");
   }
-  *out = d.release;
+  *out = w.counters;
   return MER_OK;
+}
+
+// Release flags: zeroed when (re)allocated, never cleared by kernels (they
+// hold launch epochs, which are unique, and are compared for equality).
+int ensure_release(Workspace &w, size_t words, uint64_t **out) {
+  int rc = ensure_buf(w, &w.release, &w.release_words, words, size_t(1) << 15, true, "decode release-flag allocation");
+  *out = w.release;
+  return rc;
 }
 
 int g_index(int g) { return g == 16 ? 0 : (g == 32 ? 1 : 2); }
@@ -292,9 +352,10 @@ bool decode_eligible(size_t dm, size_t dff, const uint8_t *single) {
 }
 
 // One persistent launch for n_layers MoE layers (fast path).
-int run_decode(int dtype, size_t dm, size_t dff, uint32_t n_layers, uint32_t n_tok, uint32_t top_k,
-               const LayerArgs *layers, const uint8_t *single, unsigned flags, hipStream_t st) {
-  DeviceState &dev = g_dev[g_device];
+int run_decode(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_layers, uint32_t n_tok, uint32_t top_k,
+               const LayerArgs *layers, const uint8_t *single, unsigned flags) {
+  DeviceState &dev = g_dev[g_device.load()];
+  const hipStream_t st = w.stream;
   const int fmt = fmt_of(dtype);
   DecodeParams p{};
   for (uint32_t l = 0; l < n_layers; ++l) p.layers[l] = layers[l];
@@ -360,10 +421,7 @@ int run_decode(int dtype, size_t dm, size_t dff, uint32_t n_layers, uint32_t n_t
   const size_t n_hd = L * p.n_inst * p.hblocks * kLineDwords;
   const size_t n_pa = up64(L * p.n_inst * p.d_slices * dm);
   float *scratch = nullptr;
-  if (dev.scratch_floats < n_xd + n_gp + n_hd + n_pa && capturing(st))
-    return fail(MER_ERR_PHYSICAL_CAPACITY,
-                "scratch must grow, which cannot happen under graph capture: run the same call once before capturing");
-  int rc = ensure_scratch(n_xd + n_gp + n_hd + n_pa, &scratch);
+  int rc = ensure_scratch(w, n_xd + n_gp + n_hd + n_pa, &scratch);
   if (rc) return rc;
   float *cur = scratch;
   p.xq_dig = reinterpret_cast<uint32_t *>(cur);
@@ -374,51 +432,69 @@ int run_decode(int dtype, size_t dm, size_t dff, uint32_t n_layers, uint32_t n_t
   cur += n_hd;
   p.partial = cur;
   uint32_t *counters = nullptr;
-  if ((rc = ensure_counters(p.n_counters, st, &counters))) return rc;
+  if ((rc = ensure_counters(w, p.n_counters, &counters))) return rc;
   p.counters = counters;
   // Release flags of layers, and of h slices when their count is small
   // (each flag takes a 256-byte line).
-  const size_t layer_flags = (size_t)n_layers * n_tok * kReleaseFan * kPollStride;
+  const size_t layer_flags = (size_t)n_layers * n_tok * kReleaseFan * kFlagStride;
   const size_t gd_keys = (size_t)n_layers * p.n_inst * p.d_slices;
   const bool gd_fan = gd_keys <= 1024;
-  const size_t gd_flags = gd_fan ? gd_keys * kReleaseFan * kPollStride : 0;
-  uint32_t *release = nullptr;
-  if ((rc = ensure_release(layer_flags + gd_flags, st, &release))) return rc;
+  const size_t gd_flags = gd_fan ? gd_keys * kReleaseFan * kFlagStride : 0;
+  uint64_t *release = nullptr;
+  if ((rc = ensure_release(w, layer_flags + gd_flags, &release))) return rc;
   p.release = release;
   p.gd_release = gd_fan ? release + layer_flags : nullptr;
-  p.exit_count = counters + dev.counter_words - 1;
-  p.abort_flag = counters + dev.counter_words - kPollStride;
+  uint32_t *ctl = counters + w.counter_words - kCtlLines * kPollStride;
+  p.exit_count = ctl;
+  p.abort_flag = ctl + kPollStride;
+  p.epoch_word = reinterpret_cast<uint64_t *>(ctl + 2 * kPollStride);
   p.status = dev.status;
   p.timeout_ticks = dev.clock_khz * 2000;  // 2 s per wait
-  p.trace = dev.trace;
-  p.trace_cap = dev.trace_cap;
-  if (++dev.decode_epoch == 0) ++dev.decode_epoch;  // 0 marks never-written scratch
-  p.epoch = dev.decode_epoch;
+  {
+    std::lock_guard<std::mutex> lk(g_trace_mu);
+    p.trace = g_trace;
+    p.trace_cap = g_trace_cap;
+  }
 
   const void *fn = decode_kernel_fn(fmt, gg.G, gd.G);
-  int &occ = dev.occupancy[fmt][g_index(gg.G)][g_index(gd.G)];
+  std::atomic<int> &occ_slot = dev.occupancy[fmt][g_index(gg.G)][g_index(gd.G)];
+  int occ = occ_slot.load();
   if (occ == 0) {
-    int n = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, 64, 0);
-    if (e != hipSuccess || n <= 0) return hip_fail(e, MER_ERR_RUNTIME_INVARIANT, "decode kernel occupancy query");
-    occ = n;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 64, 0);
+    if (e != hipSuccess || occ <= 0) return hip_fail(e, MER_ERR_RUNTIME_INVARIANT, "decode kernel occupancy query");
+    occ_slot.store(occ);
   }
   uint64_t grid = (uint64_t)dev.cus * (uint64_t)occ;
   if (grid > p.total_items) grid = p.total_items;
   if (grid == 0) return MER_OK;
+  // item indices run to total_items + grid (each workgroup steps once past the end)
+  if (p.total_items + grid >= (uint64_t)UINT32_MAX)
+    return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "decode launch of %llu items exceeds the 32-bit item space",
+                (unsigned long long)p.total_items);
 
-  TimedLaunch *tl = nullptr;
+  size_t tl = SIZE_MAX;
   int trc = timing_begin(STAGE_DECODE, st, &tl);
   if (trc) return trc;
-  hipError_t e = launch_decode(fn, (uint32_t)grid, p, st);
+  uintptr_t expect = UINTPTR_MAX;
+  const uintptr_t me = reinterpret_cast<uintptr_t>(st);
+  const bool plain = dev.primary_stream.compare_exchange_strong(expect, me) || expect == me;
+  hipError_t e;
+  {
+    // Decode launches from different threads are issued one at a time:
+    // without this, cooperative launches concurrent with launches from other
+    // threads left the process to crash at exit (measured on ROCm 7).
+    std::lock_guard<std::mutex> lk(g_launch_mu);
+    e = launch_decode(fn, (uint32_t)grid, p, st, !plain);
+  }
   if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "decode launch");
   return timing_end(tl, st);
 }
 
 // Enqueue prep -> gate/up -> down -> combine for n_inst expert instances.
-int run_experts(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t top_k, const void *const *table,
-                uint32_t table_len, const int32_t *ids, const uint8_t *single, const float *weights,
-                const float *x, float *out, unsigned flags, hipStream_t st, bool direct_out) {
+int run_experts(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t top_k,
+                const void *const *table, uint32_t table_len, const int32_t *ids, const uint8_t *single,
+                const float *weights, const float *x, float *out, unsigned flags, bool direct_out) {
+  const hipStream_t st = w.stream;
   const int fmt = fmt_of(dtype);
   const uint32_t n_inst = n_tokens * top_k;
   const size_t proj = div_ceil(dm * dff, 32) * block_bytes(dtype);
@@ -431,7 +507,7 @@ int run_experts(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
     la.weights = weights;
     la.x = x;
     la.out = out;
-    return run_decode(dtype, dm, dff, 1, n_tokens, top_k, &la, single, flags, st);
+    return run_decode(w, dtype, dm, dff, 1, n_tokens, top_k, &la, single, flags);
   }
 
   const ProjPlan pg = plan_projection(dff, dm, true, aligned);
@@ -452,7 +528,7 @@ int run_experts(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
   const size_t n_h = fast ? 0 : up64((size_t)n_inst * dff);
   const size_t n_p = write_direct ? 0 : up64((size_t)n_inst * slices * dm);
   float *scratch = nullptr;
-  int rc = ensure_scratch(n_ptr + n_xd + n_xs + n_hd + n_hs + n_h + n_p, &scratch);
+  int rc = ensure_scratch(w, n_ptr + n_xd + n_xs + n_hd + n_hs + n_h + n_p, &scratch);
   if (rc) return rc;
   float *cur = scratch;
   const uint8_t **inst_ptr = reinterpret_cast<const uint8_t **>(cur);
@@ -470,7 +546,7 @@ int run_experts(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
   float *partial = write_direct ? out : cur;
 
   hipError_t e;
-  TimedLaunch *tl = nullptr;
+  size_t tl = SIZE_MAX;
   int trc;
 
   PrepParams q{};
@@ -586,10 +662,11 @@ int run_experts(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
 }
 
 // Grouped multi-token path: group -> gate/up -> down -> combine.
-int run_grouped(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t top_k, const void *const *table,
-                uint32_t table_len, const int32_t *ids, const float *weights, const float *x, float *out,
-                unsigned flags, hipStream_t st) {
-  DeviceState &dev = g_dev[g_device];
+int run_grouped(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t top_k,
+                const void *const *table, uint32_t table_len, const int32_t *ids, const float *weights,
+                const float *x, float *out, unsigned flags) {
+  DeviceState &dev = g_dev[g_device.load()];
+  const hipStream_t st = w.stream;
   GroupedParams p{};
   p.table = table;
   p.table_len = table_len;
@@ -622,11 +699,8 @@ int run_grouped(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
   const size_t n_hs = up64((size_t)p.n_pairs * p.hblocks);
   const size_t n_pa = up64((size_t)p.n_pairs * dm);
   const size_t total = n_hdr + n_plist + n_ok + n_tiles + n_xg + n_xs + n_hg + n_hs + n_pa;
-  if (dev.scratch_floats < total && capturing(st))
-    return fail(MER_ERR_PHYSICAL_CAPACITY,
-                "scratch must grow, which cannot happen under graph capture: run the same call once before capturing");
   float *cur = nullptr;
-  int rc = ensure_scratch(total, &cur);
+  int rc = ensure_scratch(w, total, &cur);
   if (rc) return rc;
   p.n_tiles = reinterpret_cast<uint32_t *>(cur);
   cur += n_hdr;
@@ -647,7 +721,7 @@ int run_grouped(int dtype, size_t dm, size_t dff, uint32_t n_tokens, uint32_t to
   p.partial = cur;
 
   const int fmt = fmt_of(dtype);
-  TimedLaunch *tl = nullptr;
+  size_t tl = SIZE_MAX;
   int trc;
   hipError_t e;
   if ((trc = timing_begin(STAGE_PREP, st, &tl))) return trc;
@@ -699,16 +773,34 @@ int mer_hip_init(int device) {
 
 int mer_hip_shutdown(void) {
   std::lock_guard<std::mutex> lock(g_mu);
-  if (g_device < 0) return MER_OK;
-  DeviceState &d = g_dev[g_device];
+  const int dv = g_device.load();
+  if (dv < 0) return MER_OK;
+  DeviceState &d = g_dev[dv];
   (void)hipDeviceSynchronize();
-  if (d.scratch) (void)hipFree(d.scratch);
-  if (d.stage) (void)hipFree(d.stage);
-  if (d.router_buf) (void)hipFree(d.router_buf);
-  if (d.counters) (void)hipFree(d.counters);
-  if (d.release) (void)hipFree(d.release);
-  d = DeviceState{};
+  for (auto &kv : d.ws) {
+    std::lock_guard<std::mutex> wl(kv.second->mu);
+    free_workspace(*kv.second);
+  }
+  d.ws.clear();
+  d.ready = false;
   g_device = -1;
+  return MER_OK;
+}
+
+int mer_hip_stream_release(void *stream) {
+  int rc = require_init();
+  if (rc) return rc;
+  std::unique_ptr<Workspace> w;
+  {
+    std::lock_guard<std::mutex> lock(g_mu);
+    auto &map = g_dev[g_device.load()].ws;
+    auto it = map.find((hipStream_t)stream);
+    if (it == map.end()) return MER_OK;
+    w = std::move(it->second);
+    map.erase(it);
+  }
+  std::lock_guard<std::mutex> wl(w->mu);  // waits for a call still enqueueing on it
+  free_workspace(*w);
   return MER_OK;
 }
 
@@ -732,6 +824,7 @@ int mer_hip_take_device_status(void) {
 int mer_hip_stage_timing_enable(int enable) {
   int rc = require_init();
   if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_timing_mu);
   g_timing = enable != 0;
   g_timed_used = 0;
   return MER_OK;
@@ -740,9 +833,12 @@ int mer_hip_stage_timing_enable(int enable) {
 int mer_hip_decode_trace(void *d_records, size_t capacity, uint64_t *clock_khz) {
   int rc = require_init();
   if (rc) return rc;
-  g_dev[g_device].trace = reinterpret_cast<uint64_t *>(d_records);
-  g_dev[g_device].trace_cap = d_records ? capacity : 0;
-  if (clock_khz) *clock_khz = g_dev[g_device].clock_khz;
+  {
+    std::lock_guard<std::mutex> lk(g_trace_mu);
+    g_trace = reinterpret_cast<uint64_t *>(d_records);
+    g_trace_cap = d_records ? capacity : 0;
+  }
+  if (clock_khz) *clock_khz = g_dev[g_device.load()].clock_khz;
   return MER_OK;
 }
 
@@ -755,6 +851,7 @@ int mer_hip_stage_timing_read(double *ms, uint64_t *counts) {
   }
   hipError_t e = hipDeviceSynchronize();
   if (e != hipSuccess) return hip_fail(e, MER_ERR_DEVICE_LOST, "synchronise for stage timings");
+  std::lock_guard<std::mutex> lk(g_timing_mu);
   for (size_t i = 0; i < g_timed_used; ++i) {
     float t = 0.f;
     e = hipEventElapsedTime(&t, g_timed[i].start, g_timed[i].end);
@@ -831,13 +928,17 @@ int mer_hip_expert_forward(int dtype, const void *d_bytes, size_t len, const flo
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
   if (d_model == 0) return MER_OK;
-  if (d_ff == 0) {
-    hipError_t e = hipMemsetAsync(d_y, 0, d_model * sizeof(float), st);
+  if (d_ff == 0) {  // y = W_down * h over an empty h: zeros (a kernel, so the call can be graph-captured)
+    if (!d_y) return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
+    hipError_t e = launch_zero(d_y, d_model, st);
     return e == hipSuccess ? MER_OK : hip_fail(e, MER_ERR_SUBMISSION, "zero output");
   }
   if (!d_bytes || !d_x || !d_y) return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
-  return run_experts(dtype, d_model, d_ff, 1, 1, nullptr, 0, nullptr, (const uint8_t *)d_bytes, nullptr, d_x, d_y,
-                     0u, st, true);
+  Workspace *w = workspace_for(st);
+  if (!w) return require_init();
+  std::lock_guard<std::mutex> wl(w->mu);
+  return run_experts(*w, dtype, d_model, d_ff, 1, 1, nullptr, 0, nullptr, (const uint8_t *)d_bytes, nullptr, d_x, d_y,
+                     0u, true);
 }
 
 int mer_hip_expert_forward_host(int dtype, const void *bytes, size_t len, const float *x, size_t x_len,
@@ -868,8 +969,16 @@ int mer_hip_expert_forward_host(int dtype, const void *bytes, size_t len, const 
   e = hipMemcpy(db, bytes, need, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(dx, x, d_model * sizeof(float), hipMemcpyHostToDevice);
   if (e != hipSuccess) rc = hip_fail(e, MER_ERR_UPLOAD, "host-to-device copy");
-  if (!rc) rc = run_experts(dtype, d_model, d_ff, 1, 1, nullptr, 0, nullptr, (const uint8_t *)db, nullptr, dx, dy,
-                            0u, nullptr, true);
+  if (!rc) {
+    Workspace *w = workspace_for(nullptr);
+    if (!w) {
+      rc = require_init();
+    } else {
+      std::lock_guard<std::mutex> wl(w->mu);
+      rc = run_experts(*w, dtype, d_model, d_ff, 1, 1, nullptr, 0, nullptr, (const uint8_t *)db, nullptr, dx, dy, 0u,
+                       true);
+    }
+  }
   if (!rc) {
     e = hipMemcpy(y, dy, d_model * sizeof(float), hipMemcpyDeviceToHost);
     if (e != hipSuccess) rc = hip_fail(e, MER_ERR_READBACK_MAP, "device-to-host copy");
@@ -897,8 +1006,11 @@ int mer_hip_moe_forward(int dtype, size_t d_model, size_t d_ff, size_t n_tokens,
     return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "too many expert instances");
   if (!d_expert_table || !d_expert_ids || !d_weights || !d_x || !d_out)
     return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
-  return run_experts(dtype, d_model, d_ff, (uint32_t)n_tokens, (uint32_t)top_k, d_expert_table, (uint32_t)table_len,
-                     d_expert_ids, nullptr, d_weights, d_x, d_out, flags, (hipStream_t)stream, false);
+  Workspace *w = workspace_for((hipStream_t)stream);
+  if (!w) return require_init();
+  std::lock_guard<std::mutex> wl(w->mu);
+  return run_experts(*w, dtype, d_model, d_ff, (uint32_t)n_tokens, (uint32_t)top_k, d_expert_table,
+                     (uint32_t)table_len, d_expert_ids, nullptr, d_weights, d_x, d_out, flags, false);
 }
 
 int mer_hip_expert_batch_f16(int dtype, size_t d_model, size_t d_ff, size_t n_experts,
@@ -918,28 +1030,17 @@ int mer_hip_expert_batch_f16(int dtype, size_t d_model, size_t d_ff, size_t n_ex
   // Each expert is a one-slot token of weight 1 on its own copy of x, so
   // the routed forward's output row i is y of expert i, uncombined.
   const hipStream_t st = (hipStream_t)stream;
-  DeviceState &d = g_dev[g_device];
+  Workspace *w = workspace_for(st);
+  if (!w) return require_init();
+  std::lock_guard<std::mutex> wl(w->mu);
   const size_t need = 2 * n_experts * d_model;
-  if (d.stage_floats < need) {
-    if (capturing(st))
-      return fail(MER_ERR_PHYSICAL_CAPACITY, "the f16 staging buffer must grow, which cannot happen under graph "
-                                             "capture: run the same call once before capturing");
-    if (d.stage) {
-      hipError_t e = hipDeviceSynchronize();
-      if (e != hipSuccess) return hip_fail(e, MER_ERR_DEVICE_LOST, "synchronise before staging growth");
-      (void)hipFree(d.stage);
-      d.stage = nullptr;
-      d.stage_floats = 0;
-    }
-    hipError_t e = hipMalloc(&d.stage, need * sizeof(float));
-    if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "f16 staging allocation");
-    d.stage_floats = need;
-  }
-  float *x32 = d.stage, *y32 = d.stage + n_experts * d_model;
+  rc = ensure_buf(*w, &w->stage, &w->stage_floats, need, 0, false, "f16 staging allocation");
+  if (rc) return rc;
+  float *x32 = w->stage, *y32 = w->stage + n_experts * d_model;
   hipError_t e = launch_f16_in(d_x, d_model, n_experts, x32, st);
   if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "f16 input staging launch");
-  rc = run_experts(dtype, d_model, d_ff, (uint32_t)n_experts, 1u, d_expert_table, (uint32_t)table_len, d_expert_ids,
-                   nullptr, nullptr, x32, y32, 0u, st, false);
+  rc = run_experts(*w, dtype, d_model, d_ff, (uint32_t)n_experts, 1u, d_expert_table, (uint32_t)table_len,
+                   d_expert_ids, nullptr, nullptr, x32, y32, 0u, false);
   if (rc) return rc;
   e = launch_f16_out(y32, n_experts * d_model, d_out, st);
   if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "f16 output staging launch");
@@ -969,8 +1070,11 @@ int mer_hip_moe_grouped(int dtype, size_t d_model, size_t d_ff, size_t n_tokens,
                 kMaxGroupedExperts, table_len);
   if (!d_expert_table || !d_expert_ids || !d_weights || !d_x || !d_out)
     return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
-  return run_grouped(dtype, d_model, d_ff, (uint32_t)n_tokens, (uint32_t)top_k, d_expert_table, (uint32_t)table_len,
-                     d_expert_ids, d_weights, d_x, d_out, flags, (hipStream_t)stream);
+  Workspace *w = workspace_for((hipStream_t)stream);
+  if (!w) return require_init();
+  std::lock_guard<std::mutex> wl(w->mu);
+  return run_grouped(*w, dtype, d_model, d_ff, (uint32_t)n_tokens, (uint32_t)top_k, d_expert_table,
+                     (uint32_t)table_len, d_expert_ids, d_weights, d_x, d_out, flags);
 }
 
 int mer_hip_moe_forward_layers(int dtype, size_t d_model, size_t d_ff, size_t n_layers, size_t n_tokens,
@@ -1003,8 +1107,11 @@ int mer_hip_moe_forward_layers(int dtype, size_t d_model, size_t d_ff, size_t n_
     la[l].x = a.x;
     la[l].out = a.out;
   }
-  return run_decode(dtype, d_model, d_ff, (uint32_t)n_layers, (uint32_t)n_tokens, (uint32_t)top_k, la, nullptr,
-                    flags, (hipStream_t)stream);
+  Workspace *w = workspace_for((hipStream_t)stream);
+  if (!w) return require_init();
+  std::lock_guard<std::mutex> wl(w->mu);
+  return run_decode(*w, dtype, d_model, d_ff, (uint32_t)n_layers, (uint32_t)n_tokens, (uint32_t)top_k, la, nullptr,
+                    flags);
 }
 
 int mer_hip_route_linear_gate(const float *d_gate, size_t n_experts, size_t d_model, const float *d_x,
@@ -1049,25 +1156,15 @@ int mer_hip_route_linear_gate(const float *d_gate, size_t n_experts, size_t d_mo
     p.scaling = options->routed_scaling_factor;
   }
   p.logit_buf = d_logits;
+  Workspace *w = nullptr;
+  std::unique_lock<std::mutex> wl;
   if (!d_logits) {
-    DeviceState &d = g_dev[g_device];
-    const size_t need = n_tokens * n_experts;
-    if (d.router_floats < need) {
-      if (capturing((hipStream_t)stream))
-        return fail(MER_ERR_PHYSICAL_CAPACITY, "the router's logits buffer must grow, which cannot happen under graph "
-                                               "capture: run the same call once before capturing");
-      if (d.router_buf) {
-        hipError_t e = hipDeviceSynchronize();
-        if (e != hipSuccess) return hip_fail(e, MER_ERR_DEVICE_LOST, "synchronise before router buffer growth");
-        (void)hipFree(d.router_buf);
-        d.router_buf = nullptr;
-        d.router_floats = 0;
-      }
-      hipError_t e = hipMalloc(&d.router_buf, need * sizeof(float));
-      if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "router logits allocation");
-      d.router_floats = need;
-    }
-    p.logit_buf = d.router_buf;
+    w = workspace_for((hipStream_t)stream);
+    if (!w) return require_init();
+    wl = std::unique_lock<std::mutex>(w->mu);
+    rc = ensure_buf(*w, &w->router_buf, &w->router_floats, n_tokens * n_experts, 0, false, "router logits allocation");
+    if (rc) return rc;
+    p.logit_buf = w->router_buf;
   }
   hipError_t e = launch_router(p, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "router launch");

@@ -46,6 +46,9 @@
 
 namespace mer {
 
+// Source of the epochs the decode launches hand to their successors.
+__device__ unsigned long long g_epoch_seq;
+
 namespace {
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
@@ -135,6 +138,37 @@ __device__ bool wait_for(const DecodeParams &p, const uint32_t *ctr, uint32_t ta
   return ok != 0;
 }
 
+// Wait until the release flag *flag holds this launch's epoch (lane 0
+// polls), then acquire.  Flags are compared for equality: a flag left by any
+// other launch holds another epoch and reads as not set.  Timeout and abort
+// as wait_for.
+__device__ bool wait_flag(const DecodeParams &p, const uint64_t *flag, uint64_t epoch, uint32_t max_nap) {
+  uint32_t ok = 1;
+  if (lane_id() == 0 && ld_dev(flag) != epoch) {
+    const uint64_t t0 = wall_clock64();
+    uint32_t nap = 1, n = 0;
+    while (ld_dev(flag) != epoch) {
+      for (uint32_t i = 0; i < nap; ++i) __builtin_amdgcn_s_sleep(2);
+      if (nap < max_nap) nap <<= 1;
+      if ((++n & 15u) == 0u) {
+        if (poll(p.abort_flag) != 0u) {
+          ok = 0;
+          break;
+        }
+        if (wall_clock64() - t0 > p.timeout_ticks) {
+          set_status(p, 24u /* MER_ERR_RUNTIME_INVARIANT: dependency timeout */);
+          __hip_atomic_store(p.abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ok = 0;
+          break;
+        }
+      }
+    }
+  }
+  ok = __shfl(ok, 0, 64);
+  compiler_fence();
+  return ok != 0;
+}
+
 // Publish this wave's device-scope stores, then count one arrival.
 __device__ __forceinline__ void signal(uint32_t *ctr) {
   drain_stores();
@@ -155,15 +189,15 @@ __device__ __forceinline__ bool arrive_last(uint32_t *ctr, uint32_t expected) {
 
 // Release flag k of (layer, token): its own 256-byte line; holds the epoch
 // of the last launch whose layer was complete for that token.
-__device__ __forceinline__ uint32_t *release_flag(const DecodeParams &p, uint32_t layer, uint32_t t, uint32_t k) {
-  return p.release + (((size_t)layer * p.n_tok + t) * kReleaseFan + k) * kPollStride;
+__device__ __forceinline__ uint64_t *release_flag(const DecodeParams &p, uint32_t layer, uint32_t t, uint32_t k) {
+  return p.release + (((size_t)layer * p.n_tok + t) * kReleaseFan + k) * kFlagStride;
 }
 
 // Release flag k of the h slice (layer, instance, column slice), set when
 // all of the slice's h tiles are packed.
-__device__ __forceinline__ uint32_t *gd_flag(const DecodeParams &p, uint32_t layer, uint32_t inst, uint32_t ds,
+__device__ __forceinline__ uint64_t *gd_flag(const DecodeParams &p, uint32_t layer, uint32_t inst, uint32_t ds,
                                              uint32_t k) {
-  return p.gd_release + ((((size_t)layer * p.n_inst + inst) * p.d_slices + ds) * kReleaseFan + k) * kPollStride;
+  return p.gd_release + ((((size_t)layer * p.n_inst + inst) * p.d_slices + ds) * kReleaseFan + k) * kFlagStride;
 }
 
 // Optional per-item trace, 8 x u64 per item: {item << 32 | XCC << 16 | low
@@ -214,10 +248,11 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 
 // Quantise `nblocks` (<= 64 / groups) blocks of x into digit planes in line
-// format (dword 24 = scale, dword 25 = launch epoch); one wave, lane = group.  DEV: x is read with device-scope loads (it may have
-// been written by another wave of this launch); otherwise x is in LDS.
+// format (dword 24 = scale, dwords 25..26 = launch epoch); one wave, lane =
+// group.  DEV: x is read with device-scope loads (it may have been written
+// by another wave of this launch); otherwise x is in LDS.
 template <int FMT, bool DEV>
-__device__ __forceinline__ void pack_blocks(const float *x, uint32_t nblocks, uint32_t *dig, uint32_t epoch) {
+__device__ __forceinline__ void pack_blocks(const float *x, uint32_t nblocks, uint32_t *dig, uint64_t epoch) {
   using D = DigitTraits<FMT>;
   const uint32_t g = lane_id();
   const bool valid = g < nblocks * D::kGroups;
@@ -253,9 +288,13 @@ __device__ __forceinline__ void pack_blocks(const float *x, uint32_t nblocks, ui
     uint32_t *line = dig + (size_t)b * kLineDwords;
 #pragma unroll
     for (int k = 0; k < D::kPlanes; ++k) st_dev(line + k * D::kGroups + m, plane[k]);
-    if (m == 0)  // scale and launch epoch, one 8-byte store
-      st_dev(reinterpret_cast<uint64_t *>(line + kBlockDigitDwords),
-             (uint64_t)__float_as_uint(bs.s) | ((uint64_t)epoch << 32));
+    if (m == 0) {  // scale and launch epoch, one 16-byte store
+      const uint32_t tail[4] = {__float_as_uint(bs.s), (uint32_t)epoch, (uint32_t)(epoch >> 32), 0u};
+      __hip_atomic_store(reinterpret_cast<uint64_t *>(line + kBlockDigitDwords),
+                         (uint64_t)tail[0] | ((uint64_t)tail[1] << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(reinterpret_cast<uint64_t *>(line + kBlockDigitDwords + 2),
+                         (uint64_t)tail[2] | ((uint64_t)tail[3] << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -366,12 +405,12 @@ struct TileWalk {
 // device-scope stores do not touch this XCD's L2): such a copy carries an
 // older epoch, and the lane then reads the line again with device-scope
 // loads, which bypass the non-coherent caches.
-__device__ __forceinline__ void fetch_digits(const uint32_t *dig, size_t block0, bool valid, uint32_t epoch,
+__device__ __forceinline__ void fetch_digits(const uint32_t *dig, size_t block0, bool valid, uint64_t epoch,
                                              uint32_t (&xd)[2 * kBlockDigitDwords], float (&xsc)[2]) {
   const __amdgpu_buffer_rsrc_t r =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(dig), 0, 0x7fffffff, 0x00020000);
   const uint32_t voff = valid ? (uint32_t)(block0 * kLineDwords * 4u) : kNoChunk;
-  uint32_t tag[2];
+  uint32_t tag_lo[2], tag_hi[2];
   auto fetch = [&](auto aux) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
@@ -384,16 +423,18 @@ __device__ __forceinline__ void fetch_digits(const uint32_t *dig, size_t block0,
         xd[b * kBlockDigitDwords + 4 * k + 2] = v.z;
         xd[b * kBlockDigitDwords + 4 * k + 3] = v.w;
       }
-      const uint2 st = __builtin_bit_cast(
-          uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff + 4u * (b * kLineDwords + kBlockDigitDwords), 0,
-                                                      decltype(aux)::value));
+      const uint4 st = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 4u * (b * kLineDwords + kBlockDigitDwords), 0,
+                                                       decltype(aux)::value));
       xsc[b] = __uint_as_float(st.x);
-      tag[b] = st.y;
+      tag_lo[b] = st.y;
+      tag_hi[b] = st.z;
     }
   };
   fetch(std::integral_constant<int, 0>{});
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt and lgkmcnt unchanged
-  const bool stale = valid && (tag[0] != epoch || tag[1] != epoch);
+  const uint32_t e_lo = (uint32_t)epoch, e_hi = (uint32_t)(epoch >> 32);
+  const bool stale = valid && ((tag_lo[0] ^ e_lo) | (tag_hi[0] ^ e_hi) | (tag_lo[1] ^ e_lo) | (tag_hi[1] ^ e_hi)) != 0u;
   if (__builtin_amdgcn_ballot_w64(stale)) {
     if (stale) fetch(std::integral_constant<int, 16 /* SC1: device scope */>{});
     // Waiting here, once, also keeps the compiler's wait-count analysis from
@@ -417,7 +458,19 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
   // two more passes in flight per wave would.
   constexpr int kBuffers = 2;
 
-  for (uint64_t gi = blockIdx.x; gi < p.total_items; gi += gridDim.x) {
+  // Every wave reads the launch's epoch; the word changes only after the
+  // last wave has left (below).
+  const uint64_t epoch_v = ld_dev(p.epoch_word);
+  const uint64_t epoch = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(epoch_v >> 32)) << 32) |
+                         __builtin_amdgcn_readfirstlane((uint32_t)epoch_v);
+  // Item i goes to workgroup i mod grid.  An item waits only on items with
+  // smaller indices.  The walk drains as long as no wave waits forever on an
+  // item of a workgroup that never becomes resident: a cooperative launch
+  // makes the whole grid resident at once, and a plain launch is used only
+  // where no other persistent grid of this library can overlap it, so its
+  // pending workgroups become resident as the kernels beside it finish
+  // (launch_decode and its caller).
+  for (uint32_t gi = blockIdx.x; gi < p.total_items; gi += gridDim.x) {
     TraceMarks tm{};
     tm.start = trace_now(p);
     const uint32_t l = (uint32_t)(gi / p.items_per_layer);
@@ -433,7 +486,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
     // polls one of kReleaseFan flags (by item), so hundreds of waiting waves
     // do not all poll the line the combines count on.
     auto wait_prev_layer = [&](uint32_t t) {
-      if (l > 0) wait_for(p, release_flag(p, l - 1, t, (uint32_t)(gi % kReleaseFan)), p.epoch, kNapFlag);
+      if (l > 0) wait_flag(p, release_flag(p, l - 1, t, (uint32_t)(gi % kReleaseFan)), epoch, kNapFlag);
     };
     const bool route_after_prev = (p.flags & kFlagRouteAfterPrev) != 0;
     // Layer l's input digits of token t are complete.  Layer 0's are packed
@@ -470,14 +523,15 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       const uint32_t idx = j - p.off_p;
       const uint32_t t = idx / p.p_items;
       const uint32_t part = idx % p.p_items;
-      if (l > 0 && p.combine_packs) continue;  // packed by layer l-1's combines
-      wait_prev_layer(t);  // layers run in order: layer l reads after layer l-1 wrote
-      tm.ready = trace_now(p);
-      const uint32_t b0 = part * kPackBlocks;
-      const uint32_t nb = min(kPackBlocks, p.xblocks - b0);
-      const size_t tb = (size_t)t * p.xblocks + b0;
-      pack_blocks<FMT, true>(xsrc + (size_t)t * p.d_model + (size_t)b0 * 32, nb, xq_dig + tb * kLineDwords, p.epoch);
-      signal(cnt + p.c_p + (size_t)t * kPollStride);
+      if (l == 0 || !p.combine_packs) {  // else packed by layer l-1's combines
+        wait_prev_layer(t);  // layers run in order: layer l reads after layer l-1 wrote
+        tm.ready = trace_now(p);
+        const uint32_t b0 = part * kPackBlocks;
+        const uint32_t nb = min(kPackBlocks, p.xblocks - b0);
+        const size_t tb = (size_t)t * p.xblocks + b0;
+        pack_blocks<FMT, true>(xsrc + (size_t)t * p.d_model + (size_t)b0 * 32, nb, xq_dig + tb * kLineDwords, epoch);
+        signal(cnt + p.c_p + (size_t)t * kPollStride);
+      }
     } else if (j < p.off_d) {
       // ---- G: gate/up of one (slot, column slice, tile) -------------------
       const uint32_t idx = j - p.off_g;
@@ -504,7 +558,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       uint32_t xd[2 * kBlockDigitDwords];
       float xsc[2];
       prio_hi();
-      fetch_digits(xq_dig, (size_t)t * p.xblocks + 2 * (size_t)c, valid, p.epoch, xd, xsc);
+      fetch_digits(xq_dig, (size_t)t * p.xblocks + 2 * (size_t)c, valid, epoch, xd, xsc);
       prio_lo();
       tm.fetched = trace_now(p);
       float *gpart = p.gpart + (((size_t)l * p.n_inst + inst) * p.g_slices + gs) * 2 * p.d_ff;
@@ -539,12 +593,12 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       if (pack) {
         __syncthreads();
         const size_t hb = (size_t)inst * p.hblocks + tile;
-        pack_blocks<FMT, false>(s_h, 1, hq_dig + hb * kLineDwords, p.epoch);
+        pack_blocks<FMT, false>(s_h, 1, hq_dig + hb * kLineDwords, epoch);
         uint32_t *gd = cnt + p.c_gd + ((size_t)inst * p.d_slices + dslice) * kPollStride;
         if (p.gd_release) {
           // the last h tile of the slice releases its D items
           const uint32_t tiles = min(p.d_cps * 2, p.g_tiles - dslice * p.d_cps * 2);
-          if (arrive_last(gd, tiles) && lane < kReleaseFan) st_dev(gd_flag(p, l, inst, dslice, lane), p.epoch);
+          if (arrive_last(gd, tiles) && lane < kReleaseFan) st_dev(gd_flag(p, l, inst, dslice, lane), epoch);
         } else {
           signal(gd);
         }
@@ -574,13 +628,13 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       // the h planes of this column slice
       const uint32_t first_tile = ds * p.d_cps * 2;
       const uint32_t n_tiles = min(p.d_cps * 2, p.g_tiles - first_tile);
-      if (p.gd_release) wait_for(p, gd_flag(p, l, inst, ds, (uint32_t)(gi % kReleaseFan)), p.epoch, kNapFlag);
+      if (p.gd_release) wait_flag(p, gd_flag(p, l, inst, ds, (uint32_t)(gi % kReleaseFan)), epoch, kNapFlag);
       else wait_for(p, cnt + p.c_gd + ((size_t)inst * p.d_slices + ds) * kPollStride, n_tiles, kNapCounter);
       tm.ready = trace_now(p);
       uint32_t xd[2 * kBlockDigitDwords];
       float xsc[2];
       prio_hi();
-      fetch_digits(hq_dig, (size_t)inst * p.hblocks + 2 * (size_t)c, valid, p.epoch, xd, xsc);
+      fetch_digits(hq_dig, (size_t)inst * p.hblocks + 2 * (size_t)c, valid, epoch, xd, xsc);
       prio_lo();
       tm.fetched = trace_now(p);
       float *part = p.partial + (((size_t)l * p.n_inst + inst) * p.d_slices + ds) * p.d_model;
@@ -642,11 +696,11 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
           // or the caller's next input, into layer l+1's digit lines
           __syncthreads();
           uint32_t *next_dig = p.xq_dig + ((size_t)(l + 1) * p.n_tok * p.xblocks + (size_t)t * p.xblocks + tile) * kLineDwords;
-          pack_blocks<FMT, false>(s_h, 1, next_dig, p.epoch);
+          pack_blocks<FMT, false>(s_h, 1, next_dig, epoch);
         }
         tm.extra = trace_now(p);
         if (arrive_last(cnt + p.c_c + (size_t)t * kPollStride, p.d_tiles) && lane < kReleaseFan)
-          st_dev(release_flag(p, l, t, lane), p.epoch);
+          st_dev(release_flag(p, l, t, lane), epoch);
         compiler_fence();
       }
     }
@@ -654,11 +708,17 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
     prio_lo();
   }
 
-  // the last wave out zeroes the counters for the next launch
+  // The last wave out (every wave has read the epoch) zeroes the counters
+  // and gives the next launch on
+  // this workspace a fresh epoch, unique on the device: the top bit set
+  // keeps it apart from the host-chosen first epochs of workspaces.
   if (arrive_last(p.exit_count, gridDim.x)) {
     for (uint32_t i = lane; i < p.n_counters; i += 64) st_dev(p.counters + i, 0u);
     if (lane == 0) {
       st_dev(p.abort_flag, 0u);
+      const uint64_t seq = __hip_atomic_fetch_add(&g_epoch_seq, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      st_dev(p.epoch_word, (uint64_t)((1ull << 63) | (seq + 1)));
+      drain_stores();
       st_dev(p.exit_count, 0u);
     }
   }
@@ -687,8 +747,9 @@ const void *decode_kernel_fn(int fmt, int gg, int gd) {
   return fmt == FMT_Q4_0 ? decode_fn_fmt<FMT_Q4_0>(gg, gd) : decode_fn_fmt<FMT_Q8_0>(gg, gd);
 }
 
-hipError_t launch_decode(const void *fn, uint32_t grid, const DecodeParams &p, hipStream_t st) {
+hipError_t launch_decode(const void *fn, uint32_t grid, const DecodeParams &p, hipStream_t st, bool cooperative) {
   void *args[] = {const_cast<DecodeParams *>(&p)};
+  if (cooperative) return hipLaunchCooperativeKernel(fn, dim3(grid), dim3(64), args, 0, st);
   return hipLaunchKernel(fn, dim3(grid), dim3(64), args, 0, st);
 }
 

@@ -88,6 +88,7 @@ constexpr uint32_t kFlagRouteAfterPrev = 8u;  // layer l > 0 touches its experts
 constexpr uint32_t kMaxLayers = 64;
 constexpr uint32_t kLineDwords = 32;     // decode digit block: 24 digit dwords, scale, padding
 constexpr uint32_t kPollStride = 64;     // words between polled decode counters (one 256-byte line each)
+constexpr uint32_t kFlagStride = 32;     // 64-bit release flags between polled flags (one 256-byte line each)
 constexpr uint32_t kReleaseFan = 16;     // release flags per (layer, token), one line each
 constexpr uint32_t kCombineBatch = 16;   // partial sums a decode combine loads in one batch
 
@@ -114,10 +115,14 @@ struct DecodeParams {
   uint32_t items_per_layer, off_p, off_g, off_d;
   uint64_t total_items;
   // scratch, all [layer]-major
-  uint32_t epoch;            // launch number on this device (never 0), tags digit lines
+  // The launch's epoch is read from *epoch_word at entry by every wave; the
+  // last wave out stores a fresh value, unique on the device, for the next
+  // launch on this workspace (so a replayed HIP graph gets a new epoch too).
+  // Epochs tag digit lines and release flags; 0 is never an epoch.
+  uint64_t *epoch_word;
   // Digit planes in the decode kernel's line format: one 128-byte line per
   // 32-element block, digit dwords 0..23, the f32 block scale in dword 24 and
-  // the epoch of the launch that wrote it in dword 25.
+  // the 64-bit epoch of the launch that wrote it in dwords 25..26.
   uint32_t *xq_dig;          // [L][n_tok][xblocks][32]
   uint32_t *hq_dig;          // [L][n_inst][hblocks][32]
   float *gpart;              // [L][n_inst][g_slices][2][d_ff]  (g_slices > 1)
@@ -125,8 +130,8 @@ struct DecodeParams {
   uint32_t *counters;        // [L][cnt_per_layer], zero between launches
   uint32_t cnt_per_layer, c_p, c_ga, c_gd, c_da, c_c;
   uint32_t n_counters;
-  uint32_t *release;         // [L][n_tok][kReleaseFan] epoch flags (never cleared: older epochs read as not set)
-  uint32_t *gd_release;      // [L][n_inst][d_slices][kReleaseFan] h-slice release flags, or null (counters)
+  uint64_t *release;         // [L][n_tok][kReleaseFan] epoch flags (never cleared: other epochs read as not set)
+  uint64_t *gd_release;      // [L][n_inst][d_slices][kReleaseFan] h-slice release flags, or null (counters)
   uint32_t *exit_count;
   uint32_t *abort_flag;      // set by a timed-out wait; later waits give up
   uint32_t *status;
@@ -197,7 +202,7 @@ struct RouterParams {
 hipError_t launch_router(const RouterParams &p, hipStream_t st);
 
 const void *decode_kernel_fn(int fmt, int gg, int gd);
-hipError_t launch_decode(const void *fn, uint32_t grid, const DecodeParams &p, hipStream_t st);
+hipError_t launch_decode(const void *fn, uint32_t grid, const DecodeParams &p, hipStream_t st, bool cooperative);
 uint32_t *device_status_ptr();
 
 hipError_t launch_prep(int fmt, const PrepParams &q, uint32_t n_tokens, hipStream_t st);
@@ -211,6 +216,7 @@ hipError_t launch_fill(int fmt, uint64_t seed, uint64_t expert, uint64_t block_b
                        float lo, float hi, uint8_t *dst, hipStream_t st);
 hipError_t launch_f16_in(const uint16_t *x, size_t d_model, size_t n_rep, float *dst, hipStream_t st);
 hipError_t launch_f16_out(const float *src, size_t n, uint16_t *dst, hipStream_t st);
+hipError_t launch_zero(float *dst, size_t n, hipStream_t st);
 hipError_t read_and_clear_device_status(uint32_t *out);
 
 // Error reporting shared by the C-ABI sources: record `msg` (and a HIP

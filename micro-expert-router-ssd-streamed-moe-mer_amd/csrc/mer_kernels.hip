@@ -520,6 +520,17 @@ hipError_t launch_f16_out(const float *src, size_t n, uint16_t *dst, hipStream_t
   return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void zero_kernel(float *dst, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[i] = 0.f;
+}
+
+hipError_t launch_zero(float *dst, size_t n, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, dst, n);
+  return hipGetLastError();
+}
+
 uint32_t *device_status_ptr() {
   void *ptr = nullptr;
   if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_device_status)) != hipSuccess) return nullptr;

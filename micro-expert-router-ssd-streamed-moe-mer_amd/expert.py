@@ -281,6 +281,14 @@ def fill_synthetic(dtype: WeightDtype, seed: int, expert_index: int, n_blocks: i
     return out
 
 
+def stream_release(stream: "torch.cuda.Stream | int | None" = None) -> None:
+    """Free the library's workspace of `stream` (default: the current
+    stream); call before destroying a stream the library has used."""
+    init()
+    handle = _stream() if stream is None else (stream if isinstance(stream, int) else stream.cuda_stream)
+    _call("mer_hip_stream_release", handle)
+
+
 def take_device_status() -> None:
     """Raise the first device-side fault recorded since the last call."""
     init()

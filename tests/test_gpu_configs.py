@@ -151,3 +151,93 @@ def test_grouped_nonfinite_input_propagates(mer, oracle, gpu):
     assert_ffn_close(got[[0, 2]], want, "finite tokens")
     mer.take_device_status()
     del devs
+
+
+def _resident_stack(mer, gpu, dtype, dm, dff, n_exp, scale, seed=0xC0FFEE):
+    """n_exp experts generated on the device by the bench's generator, as
+    bench.py lays them out: expert e at byte e * expert_bytes."""
+    eb = mer.expert_weight_bytes_for(dm, dff, mer.WeightDtype(dtype))
+    nb = eb // (18 if dtype == Q4 else 34)
+    weights = torch.empty(n_exp * eb, dtype=torch.uint8, device=gpu)
+    for e in range(n_exp):
+        mer.fill_synthetic(mer.WeightDtype(dtype), seed, e, nb, scale[0], scale[1], weights[e * eb:(e + 1) * eb])
+    torch.cuda.synchronize()
+    return weights, eb
+
+
+def _layers_launch_vs_oracle(mer, oracle, gpu, dtype, dm, dff, L, E, ids, wts, xs, weights, eb, label):
+    """One mer_hip_moe_forward_layers launch over L layers with the bench's
+    flags (ACCUMULATE, every layer's routing a launch input; then again with
+    ROUTE_AFTER_PREV), against the oracle: out = sum over layers of the
+    slot-order combine of the layer's routed experts on its own input."""
+    base = weights.data_ptr()
+    tables = torch.tensor([[base + (l * E + e) * eb for e in range(E)] for l in range(L)], dtype=torch.int64,
+                          device=gpu)
+    ids_d, wts_d, xs_d = to_dev(ids, gpu), to_dev(wts, gpu), to_dev(xs, gpu)
+    out = torch.zeros((1, dm), device=gpu)
+    layers = [dict(table=tables[l], ids=ids_d[l], weights=wts_d[l], x=xs_d[l], out=out) for l in range(L)]
+    mer.moe_forward_layers(mer.WeightDtype(dtype), dm, dff, layers, accumulate=True)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().copy()
+    out.zero_()
+    mer.moe_forward_layers(mer.WeightDtype(dtype), dm, dff, layers, accumulate=True, route_after_prev=True)
+    torch.cuda.synchronize()
+    got_rap = out.cpu().numpy().copy()
+    mer.take_device_status()
+    want = np.zeros((1, dm), np.float64)
+    for l in range(L):
+        ys = []
+        for i in range(ids.shape[2]):
+            e = l * E + int(ids[l, 0, i])
+            blob = weights[e * eb:(e + 1) * eb].cpu().numpy()
+            if dtype == Q4:
+                ys.append(oracle.q4_0_reference_forward(blob, xs[l, 0], dm, dff, nthreads=16))
+            else:
+                rc, y = oracle.q8_0_direct_forward(blob, xs[l, 0], dm, dff, nthreads=16)
+                assert rc == 0
+                ys.append(y)
+        want[0] += oracle.combine_outputs(np.stack(ys), wts[l, 0]).astype(np.float64)
+    assert_ffn_close(got, want, label)
+    assert np.array_equal(got, got_rap), f"{label}: ROUTE_AFTER_PREV changed the result"
+    del tables
+
+
+def test_mixtral_32_layer_launch_full_shape(mer, oracle, gpu):
+    """BASELINE config 1 exactly as bench.py times it: 32 layers x 8
+    Mixtral-shape Q4_0 experts (25.4 GB resident), top-2 from N(0,1) logits,
+    batch 1, each layer on its own N(0,1) input, out += sum_i w_i y_i, all
+    32 layers in one persistent launch; checked against 64 oracle expert
+    forwards (inference.rs:3291-3306) combined in slot order
+    (inference.rs:4472-4491)."""
+    dm, dff, L, E, K = 4096, 14336, 32, 8, 2
+    say("mixtral 32-layer launch, full shape")
+    weights, eb = _resident_stack(mer, gpu, Q4, dm, dff, L * E, (0.005, 0.02))
+    rng = np.random.default_rng(21)
+    ids = np.zeros((L, 1, K), np.int32)
+    wts = np.zeros((L, 1, K), np.float32)
+    for l in range(L):
+        ids[l, 0], wts[l, 0] = routing.route_scores(rng.standard_normal(E).astype(np.float32), K)
+    xs = rng.standard_normal((L, 1, dm)).astype(np.float32)
+    _layers_launch_vs_oracle(mer, oracle, gpu, Q4, dm, dff, L, E, ids, wts, xs, weights, eb, "mixtral 32 layers")
+    del weights
+
+
+def test_qwen3_48_layer_launch_full_shape(mer, oracle, gpu):
+    """BASELINE config 2 at full shape and with its own weight scales
+    U(0.002, 0.01): 48 layers x 128 Qwen3-shape Q8_0 experts (30.8 GB), top-8
+    from a LinearGate [128 x 2048] ~ N(0, 0.02) per layer on an N(0,1)
+    hidden state, one launch, accumulate mode (no residual chaining, which
+    random experts at these scales would overflow); checked against 384
+    oracle forward_q8_0_direct_into runs (inference.rs:3636-3746)."""
+    dm, dff, L, E, K = 2048, 768, 48, 128, 8
+    say("qwen3 48-layer launch, full shape")
+    weights, eb = _resident_stack(mer, gpu, Q8, dm, dff, L * E, (0.002, 0.01))
+    rng = np.random.default_rng(22)
+    ids = np.zeros((L, 1, K), np.int32)
+    wts = np.zeros((L, 1, K), np.float32)
+    xs = rng.standard_normal((L, 1, dm)).astype(np.float32)
+    for l in range(L):
+        gate = (rng.standard_normal((E, dm)) * 0.02).astype(np.float32)
+        ids[l, 0], wts[l, 0] = routing.route_linear_gate(gate, xs[l, 0], K)
+    _layers_launch_vs_oracle(mer, oracle, gpu, Q8, dm, dff, L, E, ids, wts, xs, weights, eb, "qwen3 48 layers")
+    del weights
