@@ -30,10 +30,15 @@ generator (nibbles uniform, d = f16(U(0.005, 0.02))).
   cycle over 8 copies of the 128-expert layer (5.1 GB) with fresh routing and
   inputs, so no step finds its experts in the memory-side cache.
 
-Prints one JSON line.  The CPU baseline leg times the C oracle's
-restatement of the reference's CPU path on a bounded sample of the same
-experts: q4_0_cpu_reference_forward (dequantise + f32 GEMV) for Q4_0,
-forward_q8_0_direct_into's AVX2 kernel for Q8_0.
+Prints one JSON line.  Every timed step writes outputs of its own; the
+outputs of the last timed launch are read back and checked against the
+oracle (cpu_baseline.parity_worst_ratio).  The CPU baseline leg times the C
+oracle's restatement of the reference's CPU path over whole steps of the
+same workload, starting with that last timed step, on the host's cores (up
+to the 16-thread share of a one-GPU job; host fields in the line):
+q4_0_cpu_reference_forward (dequantise + f32 GEMV) for Q4_0,
+forward_q8_0_direct_into's AVX2 kernel for Q8_0.  Configs 1 and 2 also
+report the same steps under MER_MOE_ROUTE_AFTER_PREV (route_after_prev).
 """
 from __future__ import annotations
 
@@ -56,6 +61,13 @@ Q4, Q8 = 4, 5
 BLOCK_BYTES = {Q4: 18, Q8: 34}
 METRIC = "expert-FFN tokens/s + achieved HBM GB/s (% of peak), Mixtral-shape Q4_0 top-2"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_kernel_mixtral_q4_0_traffic.md")
+# What the kernels compute in: packed GGUF weights against block fixed-point
+# activations (integer digit planes), accumulated in f32.
+DTYPE_LABEL = {
+    Q4: "q4_0 weights x 22-bit block fixed-point activations, f32 accumulate",
+    Q8: "q8_0 weights x 22-bit block fixed-point activations, f32 accumulate",
+}
+DTYPE_LABEL_GROUPED = "q8_0/q4_0 weights x 24-bit block fixed-point activations (int8 MFMA), f32 accumulate"
 
 CONFIGS = {
     0: dict(workload="mixtral-expert-q4_0", dtype=Q4, d_model=4096, d_ff=14336, layers=1, experts=32, top_k=1,
@@ -80,47 +92,96 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(dtype, blobs, x_np, dm, dff, experts_per_step, budget_s, gpu_y, unit, what):
-    """Oracle (checker) timing on host cores: a bounded sample of expert FFNs.
+def host_info(threads: int) -> dict:
+    """The host the CPU baseline ran on: its thread count, the CPUs the OS
+    reports and may schedule this process on, and the CPU model string."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    return {"cores": threads, "host_cpus": os.cpu_count(), "affinity_cpus": affinity, "cpu_model": model}
 
-    Cycles through the sampled experts (at least 1 GiB of distinct blobs, so
-    the host's caches cannot hold the sample) until `budget_s` of CPU work
-    is timed; the first experts' CPU results are compared with the GPU's."""
+
+def baseline_threads() -> int:
+    """Threads for the oracle: every CPU this process may run on, capped at
+    16, the host-CPU share of a one-GPU job on the GPU boxes (more threads
+    than that share would time the scheduler, not the kernel)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_baseline(dtype, dm, dff, steps, blob_of, gpu_rows, budget_s, units_per_step, unit, what):
+    """The oracle (checker) timed on host cores over whole steps of the
+    timed workload, and the parity leg of the timed launch.
+
+    `steps` lists steps, the first being the last timed step; a step is a
+    list of output rows, a row a list of layers, a layer (x, expert keys,
+    slot weights): the row's value is the sum over its layers of the
+    slot-order combine (combine_outputs_into, inference.rs:4472-4491) of the
+    layer's experts on x.  blob_of(key) gives an expert's host bytes (fetched
+    before each step's clock starts).  The first step's rows are compared
+    with gpu_rows, the outputs the timed launch wrote.  Steps run, cycling
+    through the list, until `budget_s` of CPU work is timed (at least one)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import mer_oracle  # noqa: E402  (test infrastructure, used as the checker)
 
-    threads = max(1, min(16, os.cpu_count() or 1))
-    hosts = [b.cpu().numpy() for b in blobs]
-    times, max_err, spent, i = [], 0.0, 0.0, 0
-    while spent < budget_s or i < len(hosts):
-        host = hosts[i % len(hosts)]
-        t0 = time.perf_counter()
+    threads = baseline_threads()
+
+    def expert(blob, x):
         if dtype == Q4:
-            y = mer_oracle.q4_0_reference_forward(host, x_np, dm, dff, nthreads=threads)
-        else:
-            rc, y = mer_oracle.q8_0_direct_forward(host, x_np, dm, dff, kernel=1, nthreads=threads)
-            assert rc == 0
-        dt = time.perf_counter() - t0
-        times.append(dt)
-        spent += dt
-        if i < len(gpu_y):
+            return mer_oracle.q4_0_reference_forward(blob, x, dm, dff, nthreads=threads)
+        rc, y = mer_oracle.q8_0_direct_forward(blob, x, dm, dff, kernel=1, nthreads=threads)
+        assert rc == 0
+        return y
+
+    spent, n_steps, n_experts, worst = 0.0, 0, 0, None
+    for si in range(1 << 30):  # the steps again and again until the budget is spent
+        if n_steps and spent >= budget_s:
+            break
+        step = steps[si % len(steps)]
+        blobs = {key: blob_of(key) for row in step for _, keys, _ in row for key in keys}
+        t0 = time.perf_counter()
+        rows = []
+        for row in step:
+            acc = np.zeros(dm, np.float64)
+            for x, keys, wts in row:
+                ys = np.stack([expert(blobs[k], x) for k in keys])
+                acc += mer_oracle.combine_outputs(ys, np.asarray(wts, np.float32)).astype(np.float64)
+                n_experts += len(keys)
+            rows.append(acc)
+        spent += time.perf_counter() - t0
+        n_steps += 1
+        if si == 0:
             # the parity tests' bar: |gpu - ref| <= 1e-3 |ref| + 1e-3 max(1, 1e-3 max|ref|)
-            ref = y.astype(np.float64)
+            ref = np.stack(rows)
+            got = np.asarray(gpu_rows, np.float64).reshape(ref.shape)
             allowed = 1e-3 * np.abs(ref) + 1e-3 * max(1.0, 1e-3 * float(np.abs(ref).max()))
-            max_err = max(max_err, float((np.abs(ref - gpu_y[i]) / allowed).max()))
-        i += 1
-    per_expert = float(np.mean(times))
-    return {
-        "value": 1.0 / (per_expert * experts_per_step),
+            worst = float((np.abs(ref - got) / allowed).max())
+    out = {
+        "value": n_steps * units_per_step / spent,
         "unit": unit,
-        "cores": threads,
+        **host_info(threads),
         "kind": "port",
-        "sample": (f"{len(times)} expert FFNs ({len(hosts)} distinct experts, cycled) with {what} restated in C on "
-                   f"{threads} threads: {spent:.1f} s, mean {per_expert * 1e3:.2f} ms/expert, scaled to "
-                   f"{experts_per_step} experts/step"),
-        "ms_per_expert": per_expert * 1e3,
-        "parity_worst_ratio": max_err,
+        "sample": (f"{n_steps} whole step(s) of the timed workload ({n_experts} expert FFNs, starting with the "
+                   f"last timed step, cycling over {len(steps)} timed steps) with {what} restated in C on {threads} "
+                   f"threads: {spent:.1f} s"),
+        "ms_per_expert": spent / max(n_experts, 1) * 1e3,
+        "parity_worst_ratio": worst,
+        "parity_of": "the outputs the last timed launch wrote, against the oracle on the same step",
     }
+    return out
 
 
 def read_traffic(cfg_id: int):
@@ -201,23 +262,14 @@ def run_cache_pressure(args, cfg, mer, routing, dev, stream):
     t_comp = dec_ms * 1e-3
     overlap = (t_copy + t_comp - elapsed) / min(t_copy, t_comp) if min(t_copy, t_comp) > 0 else None
 
-    # parity leg on the last step: GPU output against the oracle for token 0
     s_last = total_steps - 1
-    sample_experts = [int(e) for e in ids[s_last, 0]]
-    gpu_tok0 = outs[s_last, 0].cpu().numpy().astype(np.float64)
-    xdev = torch.from_numpy(np.ascontiguousarray(xs[s_last, 0])).to(dev)
-    gpu_y = []
-    for e in sample_experts:
-        stage.copy_(blobs[e])
-        gpu_y.append(mer.dispatch_expert_forward(wd, stage, xdev, dm, dff).cpu().numpy().astype(np.float64))
-    combined = sum(w * y for w, y in zip(wts[s_last, 0], gpu_y))
-    comb_err = float(np.max(np.abs(combined - gpu_tok0) / (1e-3 * np.abs(combined) + 1e-3)))
+    gpu_last = outs[s_last].cpu().numpy()
 
     value = args.steps * T / elapsed
     result = {
         "metric": cfg["metric"], "value": value, "unit": cfg["unit"], "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": elapsed * 1e3 / args.steps, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "scaling": "weak", "vs_baseline": None, "data": "synthetic",
         "config": {"workload": cfg["workload"], "experts": E, "vram_slots": n_slots, "top_k": K, "batch": T,
                    "d_model": dm, "d_ff": dff, "weights": "Q4_0", "host_bytes": E * ebytes,
                    "parallelism": "single-gpu",
@@ -233,16 +285,16 @@ def run_cache_pressure(args, cfg, mer, routing, dev, stream):
                      "frac": kernel_bytes / (dec_avg_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, "traffic": None,
                      "algorithmic_bytes_per_launch": int(kernel_bytes), "avg_launch_us": dec_avg_us,
                      "note": "the step is bound by PCIe uploads of misses (see cache.h2d_*), not by this kernel"},
-        "combine_check_worst_ratio": comb_err,
     }
+    result["dtype"] = DTYPE_LABEL[dtype]
     if not args.no_cpu_baseline:
         log("cpu baseline")
-        cpu_ids = sample_experts + [e for e in range(E) if e not in sample_experts][:48 - len(sample_experts)]
-        result["cpu_baseline"] = cpu_baseline(dtype, [blobs[e] for e in cpu_ids], np.ascontiguousarray(xs[s_last, 0]),
-                                              dm, dff, T * K,
-                                              args.cpu_seconds, gpu_y, cfg["unit"],
+        steps = [[[(xs[s, t], [int(e) for e in ids[s, t]], wts[s, t])] for t in range(T)]
+                 for s in range(s_last, args.warmup - 1, -1)]
+        result["cpu_baseline"] = cpu_baseline(dtype, dm, dff, steps, lambda e: blobs[e].numpy(), gpu_last,
+                                              args.cpu_seconds, T, cfg["unit"],
                                               "the reference's q4_0_cpu_reference_forward (dequantise + f32 GEMV)")
-        result["cpu_baseline"]["sample"] += "; experts resident in host RAM (no PCIe)"
+        result["cpu_baseline"]["sample"] += "; experts read from host RAM (no PCIe)"
     cache.close()
     return result
 
@@ -350,16 +402,17 @@ def main() -> int:
     total_steps = args.warmup + args.steps
     rng_x = np.random.default_rng(args.seed + 1)
     rng_r = np.random.default_rng(args.seed + 2)
-    out = torch.zeros((1, dm), dtype=torch.float32, device=dev)
 
+    # Every step writes outputs of its own, so the outputs of the last timed
+    # launch can be read back and checked against the oracle (parity leg).
     if args.config == 0:
         # one expert per step, cycling over E distinct resident experts
         xs = rng_x.standard_normal((1, dm)).astype(np.float32)
         xs_d = torch.from_numpy(xs).to(dev)
-        y = torch.empty((dm,), dtype=torch.float32, device=dev)
+        outs = torch.zeros((total_steps, dm), dtype=torch.float32, device=dev)
         fn = lib.mer_hip_expert_forward
-        all_args = [(dtype, base + (s % E) * ebytes, ebytes, xs_d.data_ptr(), dm, dm, dff, y.data_ptr(), dm, stream)
-                    for s in range(total_steps)]
+        all_args = [(dtype, base + (s % E) * ebytes, ebytes, xs_d.data_ptr(), dm, dm, dff, outs[s].data_ptr(), dm,
+                     stream) for s in range(total_steps)]
         step_bytes = ebytes + 2 * dm * 4
         launch_bytes = step_bytes
 
@@ -368,8 +421,9 @@ def main() -> int:
             if rc:
                 mer.errors.raise_for_status(rc)
 
-        sample_experts = list(range(min(E, 16)))
-        x_ref = xs[0]
+        def step_rows(s):
+            return [[(xs[0], [s % E], np.ones(1, np.float32))]]
+
         experts_per_step = 1
         routing_desc = "none (one expert per step)"
     elif args.config == 3:
@@ -384,12 +438,12 @@ def main() -> int:
         ids_d = torch.from_numpy(ids).to(dev)
         wts_d = torch.from_numpy(wts).to(dev)
         xs_d = torch.from_numpy(xs).to(dev)
-        out = torch.zeros((T, dm), dtype=torch.float32, device=dev)
+        outs = torch.zeros((total_steps, T, dm), dtype=torch.float32, device=dev)
         distinct = np.array([len(np.unique(ids[s])) for s in range(total_steps)])
         step_bytes_list = distinct * ebytes + 2 * T * dm * 4  # distinct experts' weights + x in + out
         fn = lib.mer_hip_moe_grouped
         all_args = [(dtype, dm, dff, T, K, table[s % L].data_ptr(), E, ids_d[s].data_ptr(), wts_d[s].data_ptr(),
-                     xs_d[s].data_ptr(), out.data_ptr(), 0, stream) for s in range(total_steps)]
+                     xs_d[s].data_ptr(), outs[s].data_ptr(), 0, stream) for s in range(total_steps)]
         timed_u = distinct[args.warmup:]
         step_bytes = int(np.mean(step_bytes_list[args.warmup:]))
         launch_bytes = step_bytes
@@ -399,9 +453,9 @@ def main() -> int:
             if rc:
                 mer.errors.raise_for_status(rc)
 
-        # parity sample: the experts token 0 of step 0 routes to, on its input
-        sample_experts = [int(e) for e in ids[0, 0]]
-        x_ref = xs[0, 0]
+        def step_rows(s):
+            return [[(xs[s, t], [(s % L) * E + int(e) for e in ids[s, t]], wts[s, t])] for t in range(T)]
+
         experts_per_step = T * K
         routing_desc = ("N(0,1) logits + ln p_zipf(rank; s=1.1) over a seeded rank permutation, softmax top-8 "
                         f"renormalised; distinct experts per step {timed_u.min()}..{timed_u.max()} "
@@ -428,6 +482,8 @@ def main() -> int:
         ids_d = torch.from_numpy(ids).to(dev)
         wts_d = torch.from_numpy(wts).to(dev)
         xs_d = torch.from_numpy(xs).to(dev)
+        outs = torch.zeros((total_steps, 1, dm), dtype=torch.float32, device=dev)
+        x_of = (lambda s, l: xs[0, l, 0]) if args.config == 1 else (lambda s, l: xs[s, l, 0])
         xsel = (lambda s, l: xs_d[0, l]) if args.config == 1 else (lambda s, l: xs_d[s, l])
         per_layer_bytes = K * ebytes + 3 * dm * 4  # distinct routed experts + x in, out read + written
         step_bytes = L * per_layer_bytes
@@ -435,7 +491,8 @@ def main() -> int:
         if args.per_layer:
             fn = lib.mer_hip_moe_forward
             all_args = [[(dtype, dm, dff, 1, K, table[l].data_ptr(), E, ids_d[s, l].data_ptr(), wts_d[s, l].data_ptr(),
-                          xsel(s, l).data_ptr(), out.data_ptr(), 2, stream) for l in range(L)] for s in range(total_steps)]
+                          xsel(s, l).data_ptr(), outs[s].data_ptr(), 2, stream) for l in range(L)]
+                        for s in range(total_steps)]
             launch_bytes = per_layer_bytes
 
             def run_step(s):
@@ -450,7 +507,7 @@ def main() -> int:
                 arr = (mer._lib.MerLayerArgs * L)()
                 for l in range(L):
                     arr[l] = mer._lib.MerLayerArgs(table[l].data_ptr(), E, ids_d[s, l].data_ptr(),
-                                                   wts_d[s, l].data_ptr(), xsel(s, l).data_ptr(), out.data_ptr())
+                                                   wts_d[s, l].data_ptr(), xsel(s, l).data_ptr(), outs[s].data_ptr())
                 return arr
 
             all_args = [(dtype, dm, dff, L, 1, K, layer_array(s), flags, stream) for s in range(total_steps)]
@@ -461,9 +518,9 @@ def main() -> int:
                 if rc:
                     mer.errors.raise_for_status(rc)
 
-        # parity sample: the experts step 0 routes to in the first layers
-        sample_experts = [l * E + int(ids[0, l, 0, i]) for l in range(L) for i in range(K)][:16]
-        x_ref = xs[0, 0, 0]
+        def step_rows(s):
+            return [[(x_of(s, l), [l * E + int(e) for e in ids[s, l, 0]], wts[s, l, 0]) for l in range(L)]]
+
         experts_per_step = L * K
 
     log("warmup")
@@ -471,6 +528,8 @@ def main() -> int:
         run_step(s)
     torch.cuda.synchronize()
     mer.take_device_status()
+    outs[args.warmup:].zero_()
+    torch.cuda.synchronize()
 
     # Config 3 issues four launches per step: its value is timed without the
     # per-launch stage events, which then run over a second pass of the same
@@ -484,6 +543,7 @@ def main() -> int:
         run_step(s)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    gpu_last = outs[total_steps - 1].cpu().numpy().copy()  # what the last timed launch wrote
     if separate_stage_pass:
         mer.stage_timing_enable(True)
         for s in range(args.warmup, total_steps):
@@ -524,19 +584,6 @@ def main() -> int:
     dominant = max(stage_info, key=lambda k: stage_info[k]["avg_us"] * stage_info[k]["launches"])
     dom = stage_info[dominant]
 
-    # GPU outputs of the sampled experts on the reference input (parity leg)
-    xdev = torch.from_numpy(np.ascontiguousarray(x_ref)).to(dev)
-    if args.config == 3:
-        # each sampled expert through the grouped path: one token per pair, weight 1
-        n_s = len(sample_experts)
-        gy = mer.moe_grouped(mer.WeightDtype(dtype), dm, dff, table[0],
-                             torch.tensor(sample_experts, dtype=torch.int32, device=dev).reshape(n_s, 1),
-                             torch.ones((n_s, 1), dtype=torch.float32, device=dev), xdev.reshape(1, dm).repeat(n_s, 1))
-        gpu_y = list(gy.cpu().numpy().astype(np.float64))
-    else:
-        gpu_y = [mer.dispatch_expert_forward(mer.WeightDtype(dtype), blob(e), xdev, dm, dff).cpu().numpy()
-                 .astype(np.float64) for e in sample_experts]
-
     config = {"workload": cfg["workload"], "layers": L, "experts_per_layer": E if args.config else 1,
               "top_k": K, "d_model": dm, "d_ff": dff, "weights": "Q4_0" if dtype == Q4 else "Q8_0",
               "batch": cfg.get("tokens", 1),
@@ -561,7 +608,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": DTYPE_LABEL_GROUPED if args.config == 3 else DTYPE_LABEL[dtype],
         "data": "synthetic",
         "config": config,
         "hbm_gbps": step_bytes * steps_per_s / 1e9,  # algorithmic bytes per step x steps/s
@@ -573,6 +620,29 @@ def main() -> int:
                      "algorithmic_bytes_per_launch": stage_bytes[dominant], "avg_launch_us": dom["avg_us"]},
         "stages": stage_info,
     }
+    if args.config in (1, 2) and not args.per_layer and not args.route_after_prev:
+        # The same steps again with MER_MOE_ROUTE_AFTER_PREV: layer l reads its
+        # routing and streams its experts only once layer l-1 is complete, as
+        # a model whose routing is computed from that output must.
+        all_rap = [(a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7] | 8, a[8]) for a in all_args]
+        mer.stage_timing_enable(True)
+        torch.cuda.synchronize()
+        r0 = time.perf_counter()
+        for s in range(args.warmup, total_steps):
+            rc = fn(*all_rap[s])
+            if rc:
+                mer.errors.raise_for_status(rc)
+        torch.cuda.synchronize()
+        r1 = time.perf_counter()
+        rap_stage = mer.stage_timing_read()["decode"]
+        mer.stage_timing_enable(False)
+        mer.take_device_status()
+        rap_us = rap_stage[0] / max(rap_stage[1], 1) * 1e3
+        result["route_after_prev"] = {
+            "value": args.steps / (r1 - r0) * cfg.get("tokens", 1), "unit": cfg["unit"],
+            "ms_per_step": (r1 - r0) * 1e3 / args.steps, "avg_launch_us": rap_us,
+            "frac": launch_bytes / (rap_us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+            "note": "the same steps with MER_MOE_ROUTE_AFTER_PREV (routing known only after the previous layer)"}
     if args.config == 2:
         result["router"] = router_pass(gates, xs_d, ids, L, E, K, dm, args.warmup, min(5, args.steps))
     traffic = read_traffic(args.config) if dominant == "decode" and not args.per_layer else None
@@ -591,10 +661,16 @@ def main() -> int:
         log("cpu baseline")
         what = ("the reference's q4_0_cpu_reference_forward (dequantise + f32 GEMV)" if dtype == Q4 else
                 "the reference's forward_q8_0_direct_into AVX2 row kernels")
-        n_cpu = max(len(sample_experts), min(n_exp, -(-(1 << 30) // ebytes)))
-        cpu_experts = sample_experts + [e for e in range(n_exp) if e not in sample_experts][:n_cpu - len(sample_experts)]
-        result["cpu_baseline"] = cpu_baseline(dtype, [blob(e) for e in cpu_experts], x_ref, dm, dff,
-                                              experts_per_step, args.cpu_seconds, gpu_y, cfg["unit"], what)
+        host_blobs = {}
+
+        def blob_of(e):
+            if e not in host_blobs:
+                host_blobs[e] = weights[e * ebytes:(e + 1) * ebytes].cpu().numpy()
+            return host_blobs[e]
+
+        steps = [step_rows(s) for s in range(total_steps - 1, args.warmup - 1, -1)]
+        result["cpu_baseline"] = cpu_baseline(dtype, dm, dff, steps, blob_of, gpu_last, args.cpu_seconds,
+                                              cfg.get("tokens", 1) if args.config else 1, cfg["unit"], what)
     print(json.dumps(result), flush=True)
     return 0
 
