@@ -139,6 +139,16 @@ int mer_hip_stage_timing_read(double *ms /*[MER_STAGE_COUNT]*/, uint64_t *counts
  * reached).  NULL disables. */
 int mer_hip_decode_trace(void *d_records, size_t capacity, uint64_t *clock_khz);
 
+/* The GPT-OSS SwiGLU gate clamp: set_swiglu_limit / swiglu_limit
+ * (inference.rs:86-112).  A positive finite limit makes every later expert
+ * forward of this process compute silu(clamp(g, -limit, limit)) * u, as
+ * clamp_swiglu_gate and the Q8_0 direct path do (inference.rs:118-123,
+ * :3689-3702); any other value (0, negative, NaN, inf) removes the clamp,
+ * which is the default.  Process-wide, like the reference's global; a call
+ * reads it when it enqueues its kernels.  get returns +inf when unset. */
+int mer_set_swiglu_limit(float limit);
+float mer_get_swiglu_limit(void);
+
 /* ---- host-only sizing and validation (no GPU work) ----------------- */
 /* expert_weight_bytes_for (inference.rs:1089-1146); saturates. */
 size_t mer_expert_weight_bytes(int dtype, size_t d_model, size_t d_ff);
@@ -148,6 +158,14 @@ size_t mer_expert_weight_bytes(int dtype, size_t d_model, size_t d_ff);
  *   Q8_0: validate_q8_direct_layout (inference.rs:3349-3418). */
 int mer_validate_expert(int dtype, size_t len, size_t x_len, size_t y_len,
                         size_t d_model, size_t d_ff, size_t tolerance);
+/* summarise_output (inference.rs:3087-3106), the InferenceOutput digest the
+ * engine logs per expert output (InferenceOutput, :984-994): digest =
+ * FNV-1a-style fold of the f32 bit patterns of y[0..n) seeded with
+ * 0xcbf29ce484222325 ^ token_idx ^ expert_id; out_norm = sqrt of the f64
+ * sum of squares, rounded to f32.  y is host memory; either output may be
+ * NULL. */
+int mer_output_digest(uint64_t token_idx, uint32_t expert_id, const float *y, size_t n, uint64_t *digest,
+                      float *out_norm);
 /* routed_expert_gpu_compatibility (backend/mod.rs:4691-4719), extended:
  * Q8_0 is GPU-eligible here, and any Q4_0 shape is accepted (unaligned
  * shapes run the generic flat-layout kernel). */

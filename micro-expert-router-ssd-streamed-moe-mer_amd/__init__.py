@@ -41,9 +41,12 @@ from .expert import (
     q4_0_matvec,
     routed_expert_gpu_compatibility,
     routed_expert_matmul_batch,
+    set_swiglu_limit,
     stage_timing_enable,
     stage_timing_read,
     stream_release,
+    summarise_output,
+    swiglu_limit,
     take_device_status,
     validate_expert,
 )

@@ -103,6 +103,8 @@ SIGNATURES = {
     "mer_hip_init": (c_int, [c_int]),
     "mer_hip_shutdown": (c_int, []),
     "mer_hip_stream_release": (c_int, [c_void]),
+    "mer_set_swiglu_limit": (c_int, [c_float]),
+    "mer_get_swiglu_limit": (c_float, []),
     "mer_last_error": (ctypes.c_char_p, []),
     "mer_last_error_info": (c_int, [ctypes.POINTER(MerErrorInfo)]),
     "mer_hip_take_device_status": (c_int, []),
@@ -110,6 +112,8 @@ SIGNATURES = {
     "mer_hip_stage_timing_read": (c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_u64)]),
     "mer_hip_decode_trace": (c_int, [c_void, c_size, ctypes.POINTER(c_u64)]),
     "mer_expert_weight_bytes": (c_size, [c_int, c_size, c_size]),
+    "mer_output_digest": (c_int, [c_u64, ctypes.c_uint32, c_void, c_size, ctypes.POINTER(c_u64),
+                                  ctypes.POINTER(c_float)]),
     "mer_validate_expert": (c_int, [c_int, c_size, c_size, c_size, c_size, c_size, c_size]),
     "mer_routed_expert_gpu_compatibility": (c_int, [c_int, c_size, c_size]),
     "mer_hip_dequantize": (c_int, [c_int, c_void, c_size, c_size, c_void, c_void]),

@@ -117,6 +117,10 @@ DeviceState g_dev[64];
 // epochs with bit 63 set), so no two workspaces ever share an epoch.
 std::atomic<uint64_t> g_host_epoch{0};
 
+// The GPT-OSS SwiGLU gate clamp (set_swiglu_limit, inference.rs:90-99):
+// +inf when none is installed; read by every launch that applies SiLU.
+std::atomic<float> g_swiglu_limit{__builtin_inff()};
+
 // Serialises the enqueueing of decode launches (a leaf lock).
 std::mutex g_launch_mu;
 
@@ -358,6 +362,7 @@ int run_decode(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_layers
   const hipStream_t st = w.stream;
   const int fmt = fmt_of(dtype);
   DecodeParams p{};
+  p.swiglu_limit = g_swiglu_limit.load();
   for (uint32_t l = 0; l < n_layers; ++l) p.layers[l] = layers[l];
   p.single = single;
   p.n_layers = n_layers;
@@ -571,6 +576,7 @@ int run_experts(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_token
   if ((trc = timing_begin(STAGE_GATE_UP, st, &tl))) return trc;
   if (fast) {
     ProjParams p{};
+    p.swiglu_limit = g_swiglu_limit.load();
     p.inst_ptr = inst_ptr;
     p.n_inst = n_inst;
     p.proj_off0 = 0;
@@ -591,6 +597,7 @@ int run_experts(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_token
     e = launch_proj(fmt, true, pg, p, st);
   } else {
     GenericParams g{};
+    g.swiglu_limit = g_swiglu_limit.load();
     g.inst_ptr = inst_ptr;
     g.n_inst = n_inst;
     g.proj_off0 = 0;
@@ -611,6 +618,7 @@ int run_experts(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_token
   if ((trc = timing_begin(STAGE_DOWN, st, &tl))) return trc;
   if (fast) {
     ProjParams p{};
+    p.swiglu_limit = g_swiglu_limit.load();
     p.inst_ptr = inst_ptr;
     p.n_inst = n_inst;
     p.proj_off0 = 2 * proj;
@@ -628,6 +636,7 @@ int run_experts(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_token
     e = launch_proj(fmt, false, pd, p, st);
   } else {
     GenericParams g{};
+    g.swiglu_limit = g_swiglu_limit.load();
     g.inst_ptr = inst_ptr;
     g.n_inst = n_inst;
     g.proj_off0 = 2 * proj;
@@ -668,6 +677,7 @@ int run_grouped(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_token
   DeviceState &dev = g_dev[g_device.load()];
   const hipStream_t st = w.stream;
   GroupedParams p{};
+  p.swiglu_limit = g_swiglu_limit.load();
   p.table = table;
   p.table_len = table_len;
   p.ids = ids;
@@ -804,6 +814,15 @@ int mer_hip_stream_release(void *stream) {
   return MER_OK;
 }
 
+int mer_set_swiglu_limit(float limit) {
+  // set_swiglu_limit (inference.rs:90-99): a positive finite limit installs
+  // the clamp; anything else removes it.
+  g_swiglu_limit.store((limit > 0.0f && limit < __builtin_inff()) ? limit : __builtin_inff());
+  return MER_OK;
+}
+
+float mer_get_swiglu_limit(void) { return g_swiglu_limit.load(); }
+
 const char *mer_last_error(void) { return t_err.c_str(); }
 
 int mer_last_error_info(mer_error_info *out) {
@@ -866,6 +885,24 @@ int mer_hip_stage_timing_read(double *ms, uint64_t *counts) {
 size_t mer_expert_weight_bytes(int dtype, size_t d_model, size_t d_ff) {
   if (dtype != MER_DTYPE_Q4_0 && dtype != MER_DTYPE_Q8_0) return 0;
   return sat_mul(sat_mul(div_ceil(sat_mul(d_model, d_ff), 32), 3), block_bytes(dtype));
+}
+
+int mer_output_digest(uint64_t token_idx, uint32_t expert_id, const float *y, size_t n, uint64_t *digest,
+                      float *out_norm) {
+  // summarise_output (inference.rs:3087-3106): FNV-1a-style fold over the
+  // f32 bit patterns seeded with the token and expert, and the f64 L2 norm.
+  if (n && !y) return fail(MER_ERR_INVALID_LAYOUT, "null output vector");
+  double sum_sq = 0.0;
+  uint64_t d = 0xcbf29ce484222325ull ^ token_idx ^ (uint64_t)expert_id;
+  for (size_t i = 0; i < n; ++i) {
+    uint32_t bits;
+    memcpy(&bits, &y[i], 4);
+    sum_sq += (double)y[i] * (double)y[i];
+    d = (d ^ (uint64_t)bits) * 0x100000001b3ull;
+  }
+  if (digest) *digest = d;
+  if (out_norm) *out_norm = (float)__builtin_sqrt(sum_sq);
+  return MER_OK;
 }
 
 int mer_validate_expert(int dtype, size_t len, size_t x_len, size_t y_len, size_t d_model, size_t d_ff,

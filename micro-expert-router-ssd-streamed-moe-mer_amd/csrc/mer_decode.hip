@@ -566,7 +566,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       auto emit = [&](uint32_t r, const float (&a)[2]) {
         if (gl == 0) {
           if (single_slice) {
-            s_h[r - tile * kTileRows] = expert ? silu_mul(a[0], a[1]) : 0.f;
+            s_h[r - tile * kTileRows] = expert ? silu_mul(a[0], a[1], p.swiglu_limit) : 0.f;
           } else {
             st_dev(gpart + r, a[0]);
             st_dev(gpart + p.d_ff + r, a[1]);
@@ -587,7 +587,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
             g += ld_dev(p.gpart + base + (size_t)s * 2 * p.d_ff + r);
             u += ld_dev(p.gpart + base + (size_t)s * 2 * p.d_ff + p.d_ff + r);
           }
-          s_h[lane] = silu_mul(g, u);
+          s_h[lane] = silu_mul(g, u, p.swiglu_limit);
         }
       }
       if (pack) {

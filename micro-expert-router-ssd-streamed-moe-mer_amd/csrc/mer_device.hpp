@@ -273,7 +273,11 @@ __device__ __forceinline__ float flat_weight(const uint8_t *proj, size_t flat) {
   }
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
+// SwiGLU element: silu(clamp(g, -limit, limit)) * u.  The clamp is the
+// GPT-OSS swiglu_limit (inference.rs:86-123); limit = +inf disables it, and
+// a NaN gate stays NaN (as f32::clamp leaves it).
+__device__ __forceinline__ float silu_mul(float g, float u, float limit) {
+  g = g < -limit ? -limit : (g > limit ? limit : g);
   return g / (1.0f + __expf(-g)) * u;
 }
 

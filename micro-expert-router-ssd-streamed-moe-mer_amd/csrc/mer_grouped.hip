@@ -465,7 +465,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
       for (int i = 0; i < 8; ++i) {
         const float g = fin[(8 * m + i) * kGTok + c];
         const float u = fin[(32 + 8 * m + i) * kGTok + c];
-        h[i] = silu_mul(g, u);
+        h[i] = silu_mul(g, u, p.swiglu_limit);
       }
       const uint32_t pr = s_pair[c];
       const bool ok = pr != 0xffffffffu;

@@ -50,6 +50,7 @@ struct ProjParams {
   float *hq_scale;
   uint32_t hq_blocks;
   float *out;                // down: [n_inst][slices][rows]; gate/up: f32 h or null
+  float swiglu_limit;        // gate clamp before SiLU (+inf = none)
 };
 
 // Flat-layout fallback (any shape): f32 inputs and outputs.
@@ -63,6 +64,7 @@ struct GenericParams {
   uint32_t x_div;
   size_t x_stride;
   float *out;  // [n_inst][rows]
+  float swiglu_limit;  // gate clamp before SiLU (+inf = none)
 };
 
 struct ProjPlan {
@@ -106,6 +108,7 @@ struct DecodeParams {
   const uint8_t *single;     // single-expert mode: this blob for every slot
   uint32_t n_layers, n_tok, top_k, n_inst;
   uint32_t d_model, d_ff, flags;
+  float swiglu_limit;        // gate clamp before SiLU (+inf = none)
   size_t proj_bytes;         // bytes of one projection
   uint32_t xblocks, hblocks; // d_model / 32, d_ff / 32
   uint32_t g_chunks, g_slices, g_cps, g_tiles;  // gate/up: chunks per row, slices, chunks per slice, tiles
@@ -160,6 +163,7 @@ struct GroupedParams {
   uint32_t flags;
   uint32_t n_tok, top_k, n_pairs;
   uint32_t d_model, d_ff, xblocks, hblocks;
+  float swiglu_limit;        // gate clamp before SiLU (+inf = none)
   size_t proj_bytes;
   // scratch
   uint32_t *xg;              // x digits [n_tok][xblocks][4 k-groups][6 dwords]

@@ -229,7 +229,7 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjParams p) {
         const uint32_t r = r0 + j;
         if (r < r_end) {
           if constexpr (FUSED) {
-            const float h = silu_mul(acc[0][j], acc[1][j]);
+            const float h = silu_mul(acc[0][j], acc[1][j], p.swiglu_limit);
             s_h[r - tile_r0] = h;
             if (p.out) p.out[(size_t)inst * p.rows + r] = h;
           } else {
@@ -293,7 +293,7 @@ __global__ __launch_bounds__(256) void generic_kernel(GenericParams p) {
     ag = __builtin_fmaf(flat_weight<FMT>(g, flat), xv, ag);
     if (p.fused) au = __builtin_fmaf(flat_weight<FMT>(u, flat), xv, au);
   }
-  out[r] = p.fused ? silu_mul(ag, au) : ag;
+  out[r] = p.fused ? silu_mul(ag, au, p.swiglu_limit) : ag;
 }
 
 // out[t][j] = base + sum_i w[t,i] * sum_s partial[t,i,s][j]

@@ -87,6 +87,23 @@ def expert_weight_bytes_for(d_model: int, d_ff: int, dtype: WeightDtype) -> int:
     return int(_lib.lib().mer_expert_weight_bytes(int(dtype), d_model, d_ff))
 
 
+def summarise_output(token_idx: int, expert_id: int, y) -> tuple[int, float]:
+    """summarise_output (inference.rs:3087-3106): the (digest, out_norm) of an
+    expert output, as InferenceOutput carries them (inference.rs:984-994).
+    y: host float32 array or a torch tensor (copied to the host)."""
+    import numpy as np
+
+    if isinstance(y, torch.Tensor):
+        y = y.detach().to("cpu")
+        y = y.numpy()
+    ya = np.ascontiguousarray(np.asarray(y, np.float32).ravel())
+    d = ctypes.c_uint64()
+    n = ctypes.c_float()
+    _call("mer_output_digest", token_idx, expert_id, ya.ctypes.data if ya.size else None, ya.size, ctypes.byref(d),
+          ctypes.byref(n))
+    return int(d.value), float(n.value)
+
+
 def validate_expert(dtype: WeightDtype, length: int, x_len: int, y_len: int, d_model: int, d_ff: int,
                     tolerance: int = 0) -> None:
     """Raises the reference's typed error for an invalid expert call."""
@@ -279,6 +296,20 @@ def fill_synthetic(dtype: WeightDtype, seed: int, expert_index: int, n_blocks: i
     _call("mer_hip_fill_synthetic", int(dtype), seed, expert_index, block_begin, n_blocks, scale_lo, scale_hi,
           _ptr(out, torch.uint8), _stream())
     return out
+
+
+def set_swiglu_limit(limit: float | None) -> None:
+    """set_swiglu_limit (inference.rs:90-99): install the GPT-OSS SwiGLU gate
+    clamp for every later expert forward of this process (silu(clamp(g,
+    -limit, limit)) * u); None, or a non-positive / non-finite limit, removes
+    it."""
+    _call("mer_set_swiglu_limit", float("inf") if limit is None else float(limit))
+
+
+def swiglu_limit() -> float | None:
+    """swiglu_limit (inference.rs:103-112): the installed clamp, or None."""
+    v = _lib.lib().mer_get_swiglu_limit()
+    return None if v == float("inf") else v
 
 
 def stream_release(stream: "torch.cuda.Stream | int | None" = None) -> None:

@@ -299,6 +299,23 @@ static float dot_f32(const float *a, const float *b, size_t n) {
 /* inference.rs:1630-1634 silu: x / (1 + exp(-x)). */
 float mo_silu(float x) { return x / (1.0f + expf(-x)); }
 
+/* inference.rs:86-123: the process-wide GPT-OSS swiglu_limit.
+ * set_swiglu_limit keeps a positive finite limit and treats anything else
+ * as None (:94-99); clamp_swiglu_gate / the Q8_0 direct path apply
+ * g.clamp(-limit, limit) before silu (:118-123, :3699-3701, :3710-3713).
+ * f32::clamp leaves NaN as NaN.  pinned by: float64 brute force with the
+ * clamp on tiny experts whose gate values straddle the limit
+ * (tests/test_oracle_golden.py). */
+static float g_swiglu_limit = INFINITY;
+void mo_set_swiglu_limit(float limit) {
+  g_swiglu_limit = (limit > 0.0f && limit < INFINITY) ? limit : INFINITY;
+}
+float mo_get_swiglu_limit(void) { return g_swiglu_limit; }
+static float clamp_gate(float g) {
+  const float l = g_swiglu_limit;
+  return g < -l ? -l : (g > l ? l : g);
+}
+
 struct gemv_ctx {
   const float *w;
   const float *x;
@@ -358,7 +375,7 @@ static int dequant_forward(int dtype, const uint8_t *bytes, const float *x,
   struct gemv_ctx c1 = {wg, x, g, d_model}, c2 = {wu, x, u, d_model};
   par_row_chunks(d_ff, d_model, nthreads, gemv_rows, &c1);
   par_row_chunks(d_ff, d_model, nthreads, gemv_rows, &c2);
-  for (size_t i = 0; i < d_ff; ++i) g[i] = mo_silu(g[i]) * u[i];
+  for (size_t i = 0; i < d_ff; ++i) g[i] = mo_silu(clamp_gate(g[i])) * u[i];
   struct gemv_ctx c3 = {wd, g, y, d_ff};
   par_row_chunks(d_model, d_ff, nthreads, gemv_rows, &c3);
   free(w);
@@ -473,7 +490,7 @@ static void q8_gate_up_rows(void *p, size_t b, size_t e) {
     float g, u;
     mo_q8_0_gate_up_row(c->kernel, c->a + r * c->row_bytes, c->b + r * c->row_bytes,
                         c->x, c->cols, &g, &u);
-    c->out[r] = mo_silu(g) * u;
+    c->out[r] = mo_silu(clamp_gate(g)) * u;
   }
 }
 static void q8_down_rows(void *p, size_t b, size_t e) {
@@ -500,7 +517,7 @@ int mo_q8_0_direct_forward(const uint8_t *bytes, size_t len, const float *x,
   } else {
     q8_matvec_flat(gate, d_ff, d_model, x, gtmp);
     q8_matvec_flat(up, d_ff, d_model, x, h);
-    for (size_t i = 0; i < d_ff; ++i) h[i] = mo_silu(gtmp[i]) * h[i];
+    for (size_t i = 0; i < d_ff; ++i) h[i] = mo_silu(clamp_gate(gtmp[i])) * h[i];
   }
   if (d_ff % 32 == 0) {
     struct q8_ctx c = {kernel, down, NULL, h, y, d_ff / 32 * Q8_BYTES, d_ff};

@@ -70,6 +70,8 @@ float mo_q8_0_row_dot(int kernel, const uint8_t *row, const float *x,
 void mo_q8_0_gate_up_row(int kernel, const uint8_t *g, const uint8_t *u,
                          const float *x, size_t cols, float *gate, float *up);
 int mo_have_avx2_fma(void);
+void mo_set_swiglu_limit(float limit);
+float mo_get_swiglu_limit(void);
 float mo_silu(float x);
 void mo_combine_outputs(const float *outputs, const float *scores, size_t k,
                         size_t d, float *out);

@@ -42,6 +42,8 @@ _SIG = {
     "mo_q8_0_row_dot": (ctypes.c_float, [ctypes.c_int, _u8p, _f32p, _sz]),
     "mo_have_avx2_fma": (ctypes.c_int, []),
     "mo_silu": (ctypes.c_float, [ctypes.c_float]),
+    "mo_set_swiglu_limit": (None, [ctypes.c_float]),
+    "mo_get_swiglu_limit": (ctypes.c_float, []),
     "mo_combine_outputs": (None, [_f32p, _f32p, _sz, _sz, _f32p]),
     "mo_synth_hidden_state": (None, [ctypes.c_uint64, _sz, ctypes.c_uint64, _f32p]),
     "mo_deterministic_input": (None, [_sz, _sz, _f32p]),
@@ -181,6 +183,17 @@ def q8_0_direct_forward(blob: np.ndarray, x: np.ndarray, d_model: int, d_ff: int
 def q8_0_row_dot(kernel: int, row: np.ndarray, x: np.ndarray) -> float:
     xa = np.ascontiguousarray(x, np.float32)
     return lib().mo_q8_0_row_dot(kernel, _u8(np.ascontiguousarray(row, np.uint8)), _f(xa), xa.size)
+
+
+def set_swiglu_limit(limit) -> None:
+    """set_swiglu_limit (inference.rs:90-99); None or a non-positive /
+    non-finite limit removes the clamp."""
+    lib().mo_set_swiglu_limit(float("inf") if limit is None else float(limit))
+
+
+def swiglu_limit():
+    v = lib().mo_get_swiglu_limit()
+    return None if v == float("inf") else v
 
 
 def combine_outputs(outputs: np.ndarray, scores: np.ndarray) -> np.ndarray:

@@ -126,3 +126,23 @@ def test_product_package_does_not_reference_oracle():
             if f.endswith((".py", ".hip", ".hpp", ".cpp", ".h")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "mer_oracle" not in text and "oracle/" not in text, f
+
+
+def test_output_digest_matches_oracle_and_hand_case(mer, oracle):
+    """mer_output_digest = summarise_output (inference.rs:3087-3106): equal to
+    the oracle's (pinned by its closed form) on random, signed-zero and
+    non-finite vectors, and on y = [1.0] worked by hand: one xor of the bit
+    pattern 0x3f800000 into the seed, one multiplication by the FNV prime."""
+    import numpy as np
+
+    rng = np.random.default_rng(3)
+    cases = [rng.standard_normal(4096).astype(np.float32), np.array([-0.0, 0.0, np.inf, -np.inf, np.nan], np.float32),
+             np.zeros(0, np.float32)]
+    for i, y in enumerate(cases):
+        got = mer.summarise_output(7 + i, 3 * i, y)
+        want = oracle.output_digest(7 + i, 3 * i, y)
+        assert got[0] == want[0]
+        assert (np.isnan(got[1]) and np.isnan(want[1])) or got[1] == want[1]
+    d, norm = mer.summarise_output(2, 5, np.array([1.0], np.float32))
+    assert d == (((0xCBF29CE484222325 ^ 2 ^ 5) ^ 0x3F800000) * 0x100000001B3) % (1 << 64)
+    assert norm == 1.0

@@ -423,3 +423,51 @@ def test_null_device_pointers_rejected_before_launch(mer, gpu):
     assert lib.mer_hip_expert_batch_f16(4, 64, 64, 1, buf.data_ptr(), 1, ids.data_ptr(), None, f.data_ptr(), None) == bad
     torch.cuda.synchronize()
     mer.take_device_status()
+
+
+@pytest.mark.parametrize("path,dtype,dm,dff", [("decode", Q4, 512, 1024), ("decode", Q8, 2048, 768),
+                                               ("generic", Q4, 96, 160), ("grouped", Q8, 256, 512),
+                                               ("layers", Q4, 256, 512)])
+def test_swiglu_limit_matches_oracle(mer, oracle, gpu, path, dtype, dm, dff):
+    """mer_set_swiglu_limit: every kernel family clamps the gate before SiLU
+    as clamp_swiglu_gate does (inference.rs:86-123, :3689-3702); the limit
+    is chosen so it binds on a good part of the rows.  Removing it restores
+    the unclamped outputs bit for bit."""
+    say(f"swiglu limit path={path} dtype={dtype} dm={dm} dff={dff}")
+    n_exp, n_tok, k = 4, 3, 2
+    blobs = [make_expert(oracle, dtype, dm, dff, 60 + e) for e in range(n_exp)]
+    devs, table = _table(blobs, gpu)
+    rng = np.random.default_rng(31)
+    ids = np.stack([rng.choice(n_exp, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    w = rng.random((n_tok, k)).astype(np.float32)
+    x = (rng.standard_normal((n_tok, dm)) * 3).astype(np.float32)
+    limit = 0.5 if dtype == Q4 else 2.0
+    wd = mer.WeightDtype(dtype)
+
+    def run():
+        if path == "grouped":
+            return mer.moe_grouped(wd, dm, dff, table, to_dev(ids, gpu), to_dev(w, gpu), to_dev(x, gpu)).cpu().numpy()
+        if path == "layers":
+            outs = [torch.zeros((n_tok, dm), device=gpu) for _ in range(2)]
+            layers = [dict(table=table, ids=to_dev(ids, gpu), weights=to_dev(w, gpu), x=to_dev(x, gpu), out=outs[l])
+                      for l in range(2)]
+            mer.moe_forward_layers(wd, dm, dff, layers)
+            return outs[1].cpu().numpy()
+        return mer.moe_forward(wd, dm, dff, table, to_dev(ids, gpu), to_dev(w, gpu), to_dev(x, gpu)).cpu().numpy()
+
+    plain = run()
+    try:
+        mer.set_swiglu_limit(limit)
+        oracle.set_swiglu_limit(limit)
+        assert mer.swiglu_limit() == limit
+        got = run()
+        want = _oracle_moe(oracle, dtype, blobs, ids, w, x, dm, dff)
+    finally:
+        mer.set_swiglu_limit(None)
+        oracle.set_swiglu_limit(None)
+    assert_ffn_close(got, want, f"{path} clamped")
+    assert np.abs(got - plain).max() > 10 * ABS_TOL, "the clamp did not bind"
+    assert mer.swiglu_limit() is None
+    assert np.array_equal(run(), plain)
+    mer.take_device_status()
+    del devs

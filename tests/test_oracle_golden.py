@@ -187,7 +187,7 @@ def test_canonical_raw_cases_exact(oracle):
 
 # ---- expert forward -----------------------------------------------------
 
-def _brute_forward(dtype, blob, x, dm, dff):
+def _brute_forward(dtype, blob, x, dm, dff, limit=None):
     n = dm * dff
     nb = -(-n // 32)
     pb = nb * (18 if dtype == Q4 else 34)
@@ -200,6 +200,8 @@ def _brute_forward(dtype, blob, x, dm, dff):
         mats.append(np.concatenate(vals)[:n])
     g = mats[0].reshape(dff, dm) @ x.astype(np.float64)
     u = mats[1].reshape(dff, dm) @ x.astype(np.float64)
+    if limit is not None:
+        g = np.clip(g, -limit, limit)
     h = g / (1 + np.exp(-g)) * u
     return mats[2].reshape(dm, dff) @ h
 
@@ -248,6 +250,43 @@ def test_q8_direct_vs_float64(oracle, dm, dff):
         tol = 3e-3 * np.maximum(np.abs(want), 1.0) + 3e-5  # inference.rs:5962-5980
         assert np.all(np.abs(got - want) <= tol)
         assert _close(got, want, rel=1e-4, abs_=1e-6 * np.abs(want).max())
+
+
+def _gate_f64(dtype, blob, x, dm, dff):
+    n = dm * dff
+    vals = [_dq64(dtype, blob[b * (18 if dtype == Q4 else 34):(b + 1) * (18 if dtype == Q4 else 34)])
+            for b in range(-(-n // 32))]
+    return np.concatenate(vals)[:n].reshape(dff, dm) @ x.astype(np.float64)
+
+
+@pytest.mark.parametrize("dtype,dm,dff", [(Q4, 64, 96), (Q4, 37, 45), (Q8, 64, 96), (Q8, 37, 45)])
+def test_swiglu_limit_clamp_vs_float64(oracle, dtype, dm, dff):
+    """set_swiglu_limit / clamp_swiglu_gate (inference.rs:86-123): with a
+    limit between the median and the largest |gate| the clamp binds on part
+    of the rows, and the forward equals float64 brute force with
+    silu(clip(g, -l, l)) * u; a non-positive or non-finite limit removes it."""
+    blob = oracle.generate_synthetic_expert(Q4, 3, dm, dff) if dtype == Q4 else oracle.randomized_q8_expert(dm, dff, 77)
+    x = (oracle.synth_hidden_state(5, dm, 9) * 4).astype(np.float32)
+    g = np.abs(_gate_f64(dtype, blob, x, dm, dff))
+    limit = float(np.float32(np.quantile(g, 0.8)))
+    assert (g > limit).sum() >= dff // 8 and (g < limit).sum() >= dff // 2
+    fwd = (lambda: oracle.q4_0_reference_forward(blob, x, dm, dff)) if dtype == Q4 else \
+        (lambda: oracle.q8_0_direct_forward(blob, x, dm, dff)[1])
+    plain = fwd()
+    try:
+        oracle.set_swiglu_limit(limit)
+        assert oracle.swiglu_limit() == limit
+        got = fwd()
+        want = _brute_forward(dtype, blob, x, dm, dff, limit)
+        scale = np.abs(want).max()
+        assert np.all(np.abs(got - want) <= 1e-5 * scale + 1e-6)
+        assert np.abs(got - plain).max() > 1e-3 * scale  # the clamp changed the result
+        for off in (0.0, -1.0, float("nan"), float("inf")):
+            oracle.set_swiglu_limit(off)
+            assert oracle.swiglu_limit() is None
+            assert np.array_equal(fwd(), plain)
+    finally:
+        oracle.set_swiglu_limit(None)
 
 
 def test_q8_direct_matches_dequant_reference(oracle):

@@ -50,3 +50,43 @@ def test_skewed_stream_nan_cdf_entry_stays_in_range():
     s = routing.SkewedStream(8, 1, 1.0, 0.0, 11)
     s.cdf[3] = np.nan
     assert s.sample_rank(0.5) < s.cdf.size
+
+
+# Published SplitMix64 outputs for state 0 (tests/golden, splitmix64_seed0).
+_SM0 = [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F, 0xF88BB8A8724C81EC]
+
+
+def _streams(oracle, *args):
+    return [routing.SkewedStream(*args), oracle.SkewedStream(*args)]
+
+
+def test_skewed_stream_permutation_hand_worked(oracle):
+    """workload.rs:115-121: Durstenfeld shuffle of [0, 1, 2] driven by
+    SplitMix64 from state seed ^ 0xD1B54A32D192ED03.  With seed =
+    0xD1B54A32D192ED03 that state is 0, whose outputs are published:
+    i = 2: j = 0xE220A8397B1DCDAF % 3 = 1 -> [0, 2, 1];
+    i = 1: j = 0x6E789E6AA1B965F4 % 2 = 0 -> [2, 0, 1].
+    With zipf_s = 50 every draw is rank 0, so a 3-of-3 set is rank 0's id
+    followed by the top-up in rank order (workload.rs:162-170): the
+    permutation itself."""
+    assert _SM0[0] % 3 == 1 and _SM0[1] % 2 == 0
+    for s in _streams(oracle, 3, 3, 50.0, 0.0, 0xD1B54A32D192ED03):
+        assert s.next_experts() == [2, 0, 1]
+    assert routing.SkewedStream(3, 3, 50.0, 0.0, 0xD1B54A32D192ED03).rank_to_id == [2, 0, 1]
+
+
+def test_skewed_stream_state_offset_hand_worked(oracle):
+    """workload.rs:128, :136-140, :146-151: the draw state starts at
+    seed + 0x12345678; seed = -0x12345678 mod 2^64 makes it 0, so the unit
+    draws are the published outputs >> 11 over 2^53: 0.8833, 0.4315,
+    0.0264, 0.9709.  Uniform ranks (zipf_s = 0, cdf [1/3, 2/3, 1]), top-1,
+    stay probability 0.5: call 1 draws 0.8833 -> rank 2; calls 2 and 3 draw
+    0.4315 and 0.0264 < 0.5 and repeat the set; call 4 draws 0.9709 >= 0.5
+    and samples anew."""
+    seed = (-0x12345678) % (1 << 64)
+    u = [(v >> 11) / float(1 << 53) for v in _SM0]
+    assert u[0] > 2 / 3 and u[1] < 0.5 and u[2] < 0.5 and u[3] >= 0.5
+    perm = routing.SkewedStream(3, 3, 50.0, 0.0, seed).next_experts()  # rank order, as above
+    for s in _streams(oracle, 3, 1, 0.0, 0.5, seed):
+        seq = [s.next_experts() for _ in range(3)]
+        assert seq == [[perm[2]]] * 3
