@@ -222,6 +222,27 @@ int mer_hip_moe_forward(int dtype, size_t d_model, size_t d_ff,
                         const float *d_x, float *d_out, unsigned flags,
                         void *stream);
 
+/* mer_hip_moe_forward for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No reference counterpart: the reference's dispatch paths own
+ * their workspaces.  Same arguments, combine, flags and errors as
+ * mer_hip_moe_forward, for shapes the persistent decode kernel runs
+ * (d_model and d_ff non-zero multiples of 64).  Its scratch is one static
+ * 8 MiB device array per GPU, held until the process ends; a call whose
+ * scratch would exceed it fails with MER_ERR_SHAPE_EXCEEDS_WORKSPACE (a
+ * Mixtral-shape top-2 token needs 0.41 MiB, so up to 19 such tokens fit).  The call allocates
+ * nothing and enqueues two kernels (scratch preparation, decode).  Every
+ * call on a GPU shares that GPU's array, which keeps the last call's
+ * contents: calls that overlap on one GPU (two streams, or two threads
+ * without ordering) race and give wrong results; order them on one
+ * stream. */
+int mer_hip_moe_forward_noalloc(int dtype, size_t d_model, size_t d_ff,
+                                size_t n_tokens, size_t top_k,
+                                const void *const *d_expert_table, size_t table_len,
+                                const int32_t *d_expert_ids, const float *d_weights,
+                                const float *d_x, float *d_out, unsigned flags,
+                                void *stream);
+
 /* The GPU backend's f16-view entry points: Backend::expert_matmul /
  * routed_expert_matmul (backend/mod.rs:1095-1103, :4421-4441) for one
  * expert and routed_expert_matmul_batch_q4 (backend/mod.rs:3770-3850,

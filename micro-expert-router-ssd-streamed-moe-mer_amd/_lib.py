@@ -125,6 +125,9 @@ SIGNATURES = {
     "mer_hip_moe_forward": (
         c_int, [c_int, c_size, c_size, c_size, c_size, c_void, c_size, c_void, c_void, c_void, c_void,
                 ctypes.c_uint, c_void]),
+    "mer_hip_moe_forward_noalloc": (
+        c_int, [c_int, c_size, c_size, c_size, c_size, c_void, c_size, c_void, c_void, c_void, c_void,
+                ctypes.c_uint, c_void]),
     "mer_hip_moe_grouped": (
         c_int, [c_int, c_size, c_size, c_size, c_size, c_void, c_size, c_void, c_void, c_void, c_void,
                 ctypes.c_uint, c_void]),

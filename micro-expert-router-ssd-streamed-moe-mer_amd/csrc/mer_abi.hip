@@ -105,6 +105,9 @@ struct DeviceState {
   // and a single engine stream does not pay the cooperative launch's extra
   // ~16 us per launch.
   std::atomic<uintptr_t> primary_stream{UINTPTR_MAX};
+  // This device's copy of the no-alloc scratch array (below), from
+  // hipGetSymbolAddress at mer_hip_init.
+  uint8_t *noalloc_scratch = nullptr;
   std::unordered_map<hipStream_t, std::unique_ptr<Workspace>> ws;  // guarded by g_mu
 };
 // Lock order: g_mu, then a workspace's mutex.  Code holding a workspace's
@@ -355,13 +358,25 @@ bool decode_eligible(size_t dm, size_t dff, const uint8_t *single) {
   return dm % 64 == 0 && dff % 64 == 0 && dm > 0 && dff > 0 && dm <= MER_MAX_EXPERT_DIM && dff <= MER_MAX_EXPERT_DIM;
 }
 
-// One persistent launch for n_layers MoE layers (fast path).
-int run_decode(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_layers, uint32_t n_tok, uint32_t top_k,
-               const LayerArgs *layers, const uint8_t *single, unsigned flags) {
+// Geometry and scratch sizes of one persistent decode launch: everything
+// but the buffers, which a workspace or the no-alloc scratch provides.
+struct DecodePlan {
+  DecodeParams p;
+  int fmt;
+  SliceGeom gg, gd;
+  size_t n_xd, n_gp, n_hd, n_pa;  // floats: x digit lines, gate/up slice partials, h digit lines, down partials
+  size_t layer_flags, gd_flags;   // 64-bit release flags
+  bool gd_fan;
+  size_t floats() const { return n_xd + n_gp + n_hd + n_pa; }
+};
+
+void plan_decode(DecodePlan &pl, int dtype, size_t dm, size_t dff, uint32_t n_layers, uint32_t n_tok, uint32_t top_k,
+                 const LayerArgs *layers, const uint8_t *single, unsigned flags) {
   DeviceState &dev = g_dev[g_device.load()];
-  const hipStream_t st = w.stream;
   const int fmt = fmt_of(dtype);
-  DecodeParams p{};
+  pl.fmt = fmt;
+  DecodeParams &p = pl.p;
+  p = DecodeParams{};
   p.swiglu_limit = g_swiglu_limit.load();
   for (uint32_t l = 0; l < n_layers; ++l) p.layers[l] = layers[l];
   p.single = single;
@@ -381,7 +396,7 @@ int run_decode(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_layers
   // on the 48-layer Qwen3 decode; wider layers gain nothing).
   const uint32_t g_chunks = (uint32_t)(dm / 64);
   const bool narrow = (uint64_t)n_tok * top_k * (dff / kTileRows) < 512 && g_chunks >= 32;
-  const SliceGeom gg = slice_geom(g_chunks, narrow ? 2 : 1);
+  pl.gg = slice_geom(g_chunks, narrow ? 2 : 1);
   // Down rows longer than 64 chunks are cut into 32-chunk slices when they
   // divide evenly (Mixtral's 224 -> 7 x 32), so every lane of a 32-lane row
   // group has a chunk, as long as the combine still loads all its parts in
@@ -389,14 +404,14 @@ int run_decode(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_layers
   // 4 slices of 56 chunks).
   const uint32_t d_chunks = (uint32_t)(dff / 64);
   const bool d32 = d_chunks > 64 && d_chunks % 32 == 0 && top_k * (d_chunks / 32) <= kCombineBatch;
-  const SliceGeom gd = slice_geom(d_chunks, d32 ? d_chunks / 32 : 1);
+  pl.gd = slice_geom(d_chunks, d32 ? d_chunks / 32 : 1);
   p.g_chunks = (uint32_t)(dm / 64);
-  p.g_slices = gg.slices;
-  p.g_cps = gg.cps;
+  p.g_slices = pl.gg.slices;
+  p.g_cps = pl.gg.cps;
   p.g_tiles = (uint32_t)(dff / kTileRows);
   p.d_chunks = (uint32_t)(dff / 64);
-  p.d_slices = gd.slices;
-  p.d_cps = gd.cps;
+  p.d_slices = pl.gd.slices;
+  p.d_cps = pl.gd.cps;
   p.d_tiles = (uint32_t)(dm / kTileRows);
   const uint32_t pack_blocks = fmt == FMT_Q4_0 ? 16 : 8;
   p.p_items = (uint32_t)div_ceil(p.xblocks, pack_blocks);
@@ -421,38 +436,16 @@ int run_decode(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_layers
 
   auto up64 = [](size_t v) { return (v + 63) / 64 * 64; };
   const size_t L = n_layers;
-  const size_t n_xd = L * n_tok * p.xblocks * kLineDwords;
-  const size_t n_gp = p.g_slices > 1 ? up64(L * p.n_inst * p.g_slices * 2 * dff) : 0;
-  const size_t n_hd = L * p.n_inst * p.hblocks * kLineDwords;
-  const size_t n_pa = up64(L * p.n_inst * p.d_slices * dm);
-  float *scratch = nullptr;
-  int rc = ensure_scratch(w, n_xd + n_gp + n_hd + n_pa, &scratch);
-  if (rc) return rc;
-  float *cur = scratch;
-  p.xq_dig = reinterpret_cast<uint32_t *>(cur);
-  cur += n_xd;
-  p.gpart = cur;
-  cur += n_gp;
-  p.hq_dig = reinterpret_cast<uint32_t *>(cur);
-  cur += n_hd;
-  p.partial = cur;
-  uint32_t *counters = nullptr;
-  if ((rc = ensure_counters(w, p.n_counters, &counters))) return rc;
-  p.counters = counters;
+  pl.n_xd = L * n_tok * p.xblocks * kLineDwords;
+  pl.n_gp = p.g_slices > 1 ? up64(L * p.n_inst * p.g_slices * 2 * dff) : 0;
+  pl.n_hd = L * p.n_inst * p.hblocks * kLineDwords;
+  pl.n_pa = up64(L * p.n_inst * p.d_slices * dm);
   // Release flags of layers, and of h slices when their count is small
   // (each flag takes a 256-byte line).
-  const size_t layer_flags = (size_t)n_layers * n_tok * kReleaseFan * kFlagStride;
+  pl.layer_flags = (size_t)n_layers * n_tok * kReleaseFan * kFlagStride;
   const size_t gd_keys = (size_t)n_layers * p.n_inst * p.d_slices;
-  const bool gd_fan = gd_keys <= 1024;
-  const size_t gd_flags = gd_fan ? gd_keys * kReleaseFan * kFlagStride : 0;
-  uint64_t *release = nullptr;
-  if ((rc = ensure_release(w, layer_flags + gd_flags, &release))) return rc;
-  p.release = release;
-  p.gd_release = gd_fan ? release + layer_flags : nullptr;
-  uint32_t *ctl = counters + w.counter_words - kCtlLines * kPollStride;
-  p.exit_count = ctl;
-  p.abort_flag = ctl + kPollStride;
-  p.epoch_word = reinterpret_cast<uint64_t *>(ctl + 2 * kPollStride);
+  pl.gd_fan = gd_keys <= 1024;
+  pl.gd_flags = pl.gd_fan ? gd_keys * kReleaseFan * kFlagStride : 0;
   p.status = dev.status;
   p.timeout_ticks = dev.clock_khz * 2000;  // 2 s per wait
   {
@@ -460,9 +453,34 @@ int run_decode(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_layers
     p.trace = g_trace;
     p.trace_cap = g_trace_cap;
   }
+}
 
-  const void *fn = decode_kernel_fn(fmt, gg.G, gd.G);
-  std::atomic<int> &occ_slot = dev.occupancy[fmt][g_index(gg.G)][g_index(gd.G)];
+// Point the plan at its buffers: `f` holds pl.floats() floats, `counters`
+// p.n_counters words (zero), `ctl` the three control lines (exit count,
+// abort flag, epoch word), `release` the flags.
+void bind_decode(DecodePlan &pl, float *f, uint32_t *counters, uint32_t *ctl, uint64_t *release) {
+  DecodeParams &p = pl.p;
+  p.xq_dig = reinterpret_cast<uint32_t *>(f);
+  f += pl.n_xd;
+  p.gpart = f;
+  f += pl.n_gp;
+  p.hq_dig = reinterpret_cast<uint32_t *>(f);
+  f += pl.n_hd;
+  p.partial = f;
+  p.counters = counters;
+  p.release = release;
+  p.gd_release = pl.gd_fan ? release + pl.layer_flags : nullptr;
+  p.exit_count = ctl;
+  p.abort_flag = ctl + kPollStride;
+  p.epoch_word = reinterpret_cast<uint64_t *>(ctl + 2 * kPollStride);
+}
+
+// Grid sizing and the launch itself.
+int launch_planned(DecodePlan &pl, hipStream_t st) {
+  DeviceState &dev = g_dev[g_device.load()];
+  DecodeParams &p = pl.p;
+  const void *fn = decode_kernel_fn(pl.fmt, pl.gg.G, pl.gd.G);
+  std::atomic<int> &occ_slot = dev.occupancy[pl.fmt][g_index(pl.gg.G)][g_index(pl.gd.G)];
   int occ = occ_slot.load();
   if (occ == 0) {
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 64, 0);
@@ -493,6 +511,67 @@ int run_decode(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_layers
   }
   if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "decode launch");
   return timing_end(tl, st);
+}
+
+// One persistent launch for n_layers MoE layers (fast path) on the
+// workspace of the caller's stream.
+int run_decode(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_layers, uint32_t n_tok, uint32_t top_k,
+               const LayerArgs *layers, const uint8_t *single, unsigned flags) {
+  DecodePlan pl;
+  plan_decode(pl, dtype, dm, dff, n_layers, n_tok, top_k, layers, single, flags);
+  float *f = nullptr;
+  int rc = ensure_scratch(w, pl.floats(), &f);
+  if (rc) return rc;
+  uint32_t *counters = nullptr;
+  if ((rc = ensure_counters(w, pl.p.n_counters, &counters))) return rc;
+  uint64_t *release = nullptr;
+  if ((rc = ensure_release(w, pl.layer_flags + pl.gd_flags, &release))) return rc;
+  bind_decode(pl, f, counters, counters + w.counter_words - kCtlLines * kPollStride, release);
+  return launch_planned(pl, w.stream);
+}
+
+// ---- no-allocation decode (mer_hip_moe_forward_noalloc) --------------------
+// The decode kernel's scratch for callers that cannot allocate: one array
+// per device, held until the process ends.  In host code `scratch` names a
+// host-side stand-in; the device address comes from hipGetSymbolAddress
+// (DeviceState::noalloc_scratch), which is what kernels and copies use.
+// Layout: [0, 768) exit count, abort flag and epoch word (a 256-byte line
+// each, at fixed offsets so the epoch word survives calls of any shape),
+// then the counters, the release flags and the float region of the call.
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+int run_decode_noalloc(int dtype, size_t dm, size_t dff, uint32_t n_tok, uint32_t top_k, const LayerArgs &la,
+                       unsigned flags, hipStream_t st) {
+  DeviceState &dev = g_dev[g_device.load()];
+  uint8_t *base = dev.noalloc_scratch;
+  if (!base) return fail(MER_ERR_NOT_INITIALIZED, "the no-alloc scratch of this device is not set up");
+  DecodePlan pl;
+  plan_decode(pl, dtype, dm, dff, 1, n_tok, top_k, &la, nullptr, flags);
+  auto up256 = [](size_t b) { return (b + 255) / 256 * 256; };
+  const size_t ctl_bytes = kCtlLines * kPollStride * 4;
+  const size_t cnt_bytes = up256(pl.p.n_counters * 4);
+  const size_t flag_bytes = up256((pl.layer_flags + pl.gd_flags) * 8);
+  const size_t float_bytes = up256(pl.floats() * 4);
+  const size_t need = ctl_bytes + cnt_bytes + flag_bytes + float_bytes;
+  if (need > kNoAllocScratchBytes)
+    return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE,
+                "the no-alloc decode needs %zu bytes of scratch for d_model=%zu d_ff=%zu n_tokens=%u top_k=%u; its "
+                "static scratch holds %zu (use mer_hip_moe_forward, which grows a workspace)",
+                need, dm, dff, n_tok, top_k, kNoAllocScratchBytes);
+  uint32_t *ctl = reinterpret_cast<uint32_t *>(base);
+  uint32_t *counters = reinterpret_cast<uint32_t *>(base + ctl_bytes);
+  uint64_t *release = reinterpret_cast<uint64_t *>(base + ctl_bytes + cnt_bytes);
+  float *f = reinterpret_cast<float *>(base + ctl_bytes + cnt_bytes + flag_bytes);
+  bind_decode(pl, f, counters, ctl, release);
+  // The array keeps the last call's contents, laid out for that call's
+  // shape: clear the exit count and abort flag, this call's counters and
+  // release flags (one kernel, no memset node), and give a never-used epoch
+  // word its first epoch.
+  hipError_t e = launch_decode_scratch_prep(ctl, 2 * kPollStride, counters,
+                                            (cnt_bytes + flag_bytes) / 4, pl.p.epoch_word, st);
+  if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "no-alloc scratch preparation launch");
+  return launch_planned(pl, st);
 }
 
 // Enqueue prep -> gate/up -> down -> combine for n_inst expert instances.
@@ -532,10 +611,10 @@ int run_experts(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_token
   const size_t n_hs = fast ? up64((size_t)n_inst * hblocks) : 0;
   const size_t n_h = fast ? 0 : up64((size_t)n_inst * dff);
   const size_t n_p = write_direct ? 0 : up64((size_t)n_inst * slices * dm);
-  float *scratch = nullptr;
-  int rc = ensure_scratch(w, n_ptr + n_xd + n_xs + n_hd + n_hs + n_h + n_p, &scratch);
+  float *scr = nullptr;
+  int rc = ensure_scratch(w, n_ptr + n_xd + n_xs + n_hd + n_hs + n_h + n_p, &scr);
   if (rc) return rc;
-  float *cur = scratch;
+  float *cur = scr;
   const uint8_t **inst_ptr = reinterpret_cast<const uint8_t **>(cur);
   cur += n_ptr;
   uint32_t *xq_dig = reinterpret_cast<uint32_t *>(cur);
@@ -776,6 +855,12 @@ int mer_hip_init(int device) {
     g_dev[device].clock_khz = (uint64_t)khz;
   g_dev[device].status = device_status_ptr();
   if (!g_dev[device].status) return fail(MER_ERR_RUNTIME_INVARIANT, "device status symbol not found");
+  if (!g_dev[device].noalloc_scratch) {  // once per device, with the device current
+    uint8_t *ptr = nullptr;
+    e = hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return hip_fail(e, MER_ERR_RUNTIME_INVARIANT, "no-alloc scratch symbol address");
+    g_dev[device].noalloc_scratch = ptr;
+  }
   g_dev[device].ready = true;
   g_device = device;
   return ok();
@@ -1048,6 +1133,39 @@ int mer_hip_moe_forward(int dtype, size_t d_model, size_t d_ff, size_t n_tokens,
   std::lock_guard<std::mutex> wl(w->mu);
   return run_experts(*w, dtype, d_model, d_ff, (uint32_t)n_tokens, (uint32_t)top_k, d_expert_table,
                      (uint32_t)table_len, d_expert_ids, nullptr, d_weights, d_x, d_out, flags, false);
+}
+
+int mer_hip_moe_forward_noalloc(int dtype, size_t d_model, size_t d_ff, size_t n_tokens, size_t top_k,
+                                const void *const *d_expert_table, size_t table_len, const int32_t *d_expert_ids,
+                                const float *d_weights, const float *d_x, float *d_out, unsigned flags,
+                                void *stream) {
+  int rc = require_init();
+  if (rc) return rc;
+  if (dtype != MER_DTYPE_Q4_0 && dtype != MER_DTYPE_Q8_0)
+    return fail(MER_ERR_UNSUPPORTED_DTYPE, "unsupported expert dtype %d", dtype);
+  rc = mer_routed_expert_gpu_compatibility(dtype, d_model, d_ff);
+  if (rc) return rc;
+  if (flags & ~3u) return fail(MER_ERR_INVALID_LAYOUT, "unknown flags 0x%x", flags);
+  if ((flags & 3u) == 3u) return fail(MER_ERR_INVALID_LAYOUT, "RESIDUAL and ACCUMULATE are exclusive");
+  if (!decode_eligible(d_model, d_ff, nullptr))
+    return fail(MER_ERR_INVALID_LAYOUT,
+                "the no-alloc entry point runs the decode kernel only: d_model and d_ff must be non-zero multiples "
+                "of 64, got %zu, %zu",
+                d_model, d_ff);
+  if (n_tokens == 0 || top_k == 0) return MER_OK;
+  if (n_tokens * top_k > (1u << 16) || table_len > UINT32_MAX)
+    return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "too many expert instances");
+  if (!d_expert_table || !d_expert_ids || !d_weights || !d_x || !d_out)
+    return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
+  LayerArgs la{};
+  la.table = d_expert_table;
+  la.table_len = (uint32_t)table_len;
+  la.ids = d_expert_ids;
+  la.weights = d_weights;
+  la.x = d_x;
+  la.out = d_out;
+  return run_decode_noalloc(dtype, d_model, d_ff, (uint32_t)n_tokens, (uint32_t)top_k, la, flags,
+                            (hipStream_t)stream);
 }
 
 int mer_hip_expert_batch_f16(int dtype, size_t d_model, size_t d_ff, size_t n_experts,

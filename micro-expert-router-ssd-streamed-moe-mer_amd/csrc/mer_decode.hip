@@ -724,6 +724,30 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
   }
 }
 
+// Prepares decode scratch whose earlier contents belong to calls of other
+// shapes (the no-alloc entry point's static array): zeroes n_ctl words at
+// ctl (exit count, abort flag) and n_zero words at zero (counters, release
+// flags), and gives an epoch word that has never been used (0) its first
+// epoch.
+__global__ __launch_bounds__(256) void decode_scratch_prep_kernel(uint32_t *ctl, uint32_t n_ctl, uint32_t *zero,
+                                                                  size_t n_zero, uint64_t *epoch_word) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n_ctl) ctl[i] = 0u;
+  if (i < n_zero) zero[i] = 0u;
+  if (i == 0 && *epoch_word == 0) {
+    const uint64_t seq = __hip_atomic_fetch_add(&g_epoch_seq, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *epoch_word = (uint64_t)((1ull << 63) | (seq + 1));
+  }
+}
+
+hipError_t launch_decode_scratch_prep(uint32_t *ctl, uint32_t n_ctl, uint32_t *zero, size_t n_zero,
+                                      uint64_t *epoch_word, hipStream_t st) {
+  const size_t n = n_zero > n_ctl ? n_zero : n_ctl;
+  hipLaunchKernelGGL(decode_scratch_prep_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, ctl, n_ctl,
+                     zero, n_zero, epoch_word);
+  return hipGetLastError();
+}
+
 template <int FMT, int GG, int GD>
 static const void *decode_fn() {
   return reinterpret_cast<const void *>(&decode_kernel<FMT, GG, GD>);
