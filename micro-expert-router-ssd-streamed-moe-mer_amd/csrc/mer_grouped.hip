@@ -395,7 +395,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
   auto stage = [&](uint32_t s, typename Stager<FMT>::Buf &w) {
     sg.store(w, lq, ld);
     __syncthreads();
-    if (s + 2 < n_stages) sg.load(s + 2, row_chunks, FUSED, w);
     const uint32_t nb = min(kGStageBlocks, kblocks - s * kGStageBlocks);
 #pragma unroll
     for (int j = 0; j < kGWaveBlocks; ++j) {
@@ -421,7 +420,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
         }
       }
     }
+    // Next stage's B operands first, then the weight refill of stage s + 2:
+    // loads retire in issue order, so stage s + 1's MFMAs, which wait for
+    // the B operands, then do not also wait for stage s + 2's weights, and
+    // two weight stages stay in flight.
     if (s + 1 < n_stages) load_b(s + 1);
+    if (s + 2 < n_stages) sg.load(s + 2, row_chunks, FUSED, w);
     __syncthreads();  // LDS slab consumed before the next store
   };
   for (uint32_t s = 0; s < n_stages; s += 2) {
