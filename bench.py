@@ -359,6 +359,9 @@ def main() -> int:
     ap.add_argument("--route-after-prev", action="store_true",
                     help="layer l's routing is read and its experts streamed only after layer l-1's output is "
                          "complete (MER_MOE_ROUTE_AFTER_PREV), as when routing is computed from that output")
+    ap.add_argument("--no-route-after-prev-pass", action="store_true",
+                    help="skip the second pass of configs 1 and 2 under MER_MOE_ROUTE_AFTER_PREV (for profiler runs "
+                         "whose per-kernel averages should cover the timed launches only)")
     ap.add_argument("--per-layer", action="store_true",
                     help="one mer_hip_moe_forward call per layer instead of one multi-layer launch per token")
     args = ap.parse_args()
@@ -620,7 +623,7 @@ def main() -> int:
                      "algorithmic_bytes_per_launch": stage_bytes[dominant], "avg_launch_us": dom["avg_us"]},
         "stages": stage_info,
     }
-    if args.config in (1, 2) and not args.per_layer and not args.route_after_prev:
+    if args.config in (1, 2) and not args.per_layer and not args.route_after_prev and not args.no_route_after_prev_pass:
         # The same steps again with MER_MOE_ROUTE_AFTER_PREV: layer l reads its
         # routing and streams its experts only once layer l-1 is complete, as
         # a model whose routing is computed from that output must.
