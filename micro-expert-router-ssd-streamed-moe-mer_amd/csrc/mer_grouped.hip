@@ -57,6 +57,13 @@ constexpr uint32_t kGRows = 64;          // weight rows staged per workgroup
 // stages with one in flight (measured on the 64-token Qwen3 batch: down
 // 39 -> 36 us, 493K -> 508K tokens/s; gate/up unchanged).
 constexpr uint32_t kGStageBlocks = 8;
+#ifndef MER_G_INFLIGHT_GU
+#define MER_G_INFLIGHT_GU 2
+#endif
+#ifndef MER_G_INFLIGHT_DN
+#define MER_G_INFLIGHT_DN 2
+#endif
+constexpr int kGWavesPerEu = 4;
 constexpr uint32_t kGStageChunks = kGStageBlocks / 2;  // two-block chunks per row per stage
 constexpr int kGChunksPerThread = (int)(kGRows * kGStageChunks / 256);
 constexpr int kGWaveBlocks = (int)(kGStageBlocks / 4);  // blocks of a stage per wave
@@ -234,42 +241,46 @@ template <int FMT>
 struct Stager {
   using T = FmtTraits<FMT>;
   static constexpr int kDw = T::kChunkDwords;
-  __amdgpu_buffer_rsrc_t rsrc[2];
-  uint32_t voff[kGChunksPerThread];      // byte offset of this thread's chunk c (stage 0), or kNoChunkG
-  uint32_t srow[kGChunksPerThread], schunk[kGChunksPerThread];
+  __amdgpu_buffer_rsrc_t rsrc;           // one descriptor for the whole slab (uniform, so no per-lane waterfall)
+  uint32_t voff[kGChunksPerThread];      // byte offset of this thread's chunk c (stage 0)
+  uint32_t schunk[kGChunksPerThread];
+  uint32_t srow[kGChunksPerThread];
   using Buf = uint32_t[kGChunksPerThread][kDw];
 
-  // fused: slab rows 0..31 come from base0 (gate), rows 32..63 from base1
-  // (up), both starting at row 0; otherwise all 64 rows from base0.
-  __device__ __forceinline__ void init(const uint8_t *base0, const uint8_t *base1, uint32_t row_bytes, bool fused) {
-    rsrc[0] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base0), 0, 0x7fffffff, 0x00020000);
-    rsrc[1] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base1), 0, 0x7fffffff, 0x00020000);
+  // fused: slab rows 0..31 are gate rows starting at base, rows 32..63 the
+  // same up rows, up_off bytes further; otherwise 64 consecutive rows.
+  __device__ __forceinline__ void init(const uint8_t *base, uint32_t up_off, uint32_t row_bytes, bool fused) {
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, 0x7fffffff, 0x00020000);
 #pragma unroll
     for (int i = 0; i < kGChunksPerThread; ++i) {
       const uint32_t c = threadIdx.x + 256u * i;  // chunk of the slab: row c / kGStageChunks
       srow[i] = c / kGStageChunks;
       schunk[i] = c % kGStageChunks;
-      const uint32_t r = fused ? srow[i] % 32 : srow[i];
-      voff[i] = r * row_bytes + schunk[i] * (uint32_t)T::kChunkBytes;
+      const bool up = fused && srow[i] >= 32;
+      const uint32_t r = up ? srow[i] - 32 : srow[i];
+      voff[i] = (up ? up_off : 0u) + r * row_bytes + schunk[i] * (uint32_t)T::kChunkBytes;
     }
   }
 
-  // Issue the loads of stage s (its kGStageChunks chunks of each row) into w.
-  __device__ __forceinline__ void load(uint32_t s, uint32_t row_chunks, bool fused, Buf &w) const {
+  // Issue the loads of stage s (its kGStageChunks chunks of each row) into
+  // w.  Chunks past the row's end (and every chunk of a stage past the
+  // last) read zeros, so the loads are issued unconditionally: w is
+  // redefined on every path, which keeps the register buffers in place
+  // instead of merging two versions of them after a branch.
+  __device__ __forceinline__ void load(uint32_t s, uint32_t row_chunks, Buf &w) const {
 #pragma unroll
     for (int i = 0; i < kGChunksPerThread; ++i) {
-      const int which = fused && srow[i] >= 32 ? 1 : 0;
       const bool ok = s * kGStageChunks + schunk[i] < row_chunks;
       const uint32_t off = ok ? voff[i] + s * kGStageChunks * (uint32_t)T::kChunkBytes : kNoChunkG;
 #pragma unroll
       for (int v = 0; v < kDw / 4; ++v) {
-        const uint4 q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc[which], off + 16 * v, 0, 0));
+        const uint4 q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off + 16 * v, 0, 0));
         w[i][4 * v] = q.x;
         w[i][4 * v + 1] = q.y;
         w[i][4 * v + 2] = q.z;
         w[i][4 * v + 3] = q.w;
       }
-      w[i][kDw - 1] = __builtin_amdgcn_raw_buffer_load_b32(rsrc[which], off + 16 * (kDw / 4), 0, 0);
+      w[i][kDw - 1] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, off + 16 * (kDw / 4), 0, 0);
     }
   }
 
@@ -321,7 +332,7 @@ struct Stager {
 // writes h = silu(g) * u for 32 rows = one block per pair.  Otherwise 64
 // down rows; the epilogue writes w_i * y_i per pair.
 template <int FMT, bool FUSED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void gproj_kernel(GroupedParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerEu))) void gproj_kernel(GroupedParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t lq[kGRows * kGRowStride];
   __shared__ __attribute__((aligned(16))) float ld[kGStageBlocks * kGScaleStride];
   __shared__ uint32_t s_pair[kGTok];
@@ -339,17 +350,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
   const uint32_t row_bytes = kblocks * (uint32_t)FmtTraits<FMT>::kBlockBytes;
   Stager<FMT> sg;
   if constexpr (FUSED) {
-    const uint8_t *g = gt.blob + (size_t)rt * 32 * row_bytes;
-    sg.init(g, g + p.proj_bytes, row_bytes, true);
+    sg.init(gt.blob + (size_t)rt * 32 * row_bytes, (uint32_t)p.proj_bytes, row_bytes, true);
   } else {
-    const uint8_t *d = gt.blob + 2 * p.proj_bytes + (size_t)rt * kGRows * row_bytes;
-    sg.init(d, d, row_bytes, false);
+    sg.init(gt.blob + 2 * p.proj_bytes + (size_t)rt * kGRows * row_bytes, 0u, row_bytes, false);
   }
   const uint32_t n_stages = (kblocks + kGStageBlocks - 1) / kGStageBlocks;
-  // Two stages in flight: stage s + 2 loads into the buffer stage s leaves.
-  typename Stager<FMT>::Buf wbuf[2];
-  sg.load(0, row_chunks, FUSED, wbuf[0]);
-  if (n_stages > 1) sg.load(1, row_chunks, FUSED, wbuf[1]);
+  // kGInFlight stages in flight: stage s + kGInFlight loads into the buffer
+  constexpr int kGInFlight = FUSED ? MER_G_INFLIGHT_GU : MER_G_INFLIGHT_DN;
+  // stage s leaves.
+  typename Stager<FMT>::Buf wbuf[kGInFlight];
   __syncthreads();  // s_pair
 
   // B operands: the lane's column is pair s_pair[lane % 16]; its k-group is lane / 16
@@ -374,25 +383,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[a][i] = 0.f;
 
-  // B operands of this wave's blocks of stage s (wave, wave + 4, ...),
-  // loaded one stage ahead: the loads of stage s + 1 are issued right after
-  // stage s's MFMAs, so they arrive during the slab store.
-  uint2 bv[kGWaveBlocks][3];
-  float bs[kGWaveBlocks];
-  auto load_b = [&](uint32_t s) {
-    const uint32_t nb = min(kGStageBlocks, kblocks - s * kGStageBlocks);
+  // B operands of this wave's blocks of stage s (wave, wave + 4, ...), in
+  // a ring of kGInFlight slots loaded as far ahead as the weights: stage
+  // s + kGInFlight's B operands are issued right after stage s's MFMAs,
+  // just before its weight refill.  A lane without a valid block reads
+  // block 0 of its record and gets a zero scale.
+  uint2 bv[kGInFlight][kGWaveBlocks][3];
+  float bs[kGInFlight][kGWaveBlocks];
+  bool bok[kGInFlight][kGWaveBlocks];
+  auto load_b = [&](uint32_t s, int slot) {
+    const uint32_t left = s < n_stages ? kblocks - s * kGStageBlocks : 0u;
 #pragma unroll
     for (int j = 0; j < kGWaveBlocks; ++j) {
       const uint32_t b = wave + 4 * j;
-      const bool ok = col_ok && b < nb;
-      const uint32_t gb = s * kGStageBlocks + b;
+      bok[slot][j] = col_ok && b < left;
+      const uint32_t gb = bok[slot][j] ? s * kGStageBlocks + b : 0u;
 #pragma unroll
-      for (int k = 0; k < 3; ++k) bv[j][k] = ok ? vdig[(size_t)gb * 2 * kGRec + k] : make_uint2(0, 0);
-      bs[j] = ok ? vsc[gb] : 0.f;
+      for (int k = 0; k < 3; ++k) bv[slot][j][k] = vdig[(size_t)gb * 2 * kGRec + k];
+      bs[slot][j] = vsc[gb];
     }
   };
-  load_b(0);
-  auto stage = [&](uint32_t s, typename Stager<FMT>::Buf &w) {
+  // Issue order B(0), W(0), B(1), W(1), ...: the order in which the loop
+  // below leaves each stage's loads outstanding, so the wait counts are the
+  // same on the first round as on every later one.
+#pragma unroll
+  for (int b = 0; b < kGInFlight; ++b) {
+    load_b(b, b);
+    sg.load(b, row_chunks, wbuf[b]);
+  }
+  auto stage = [&](uint32_t s, typename Stager<FMT>::Buf &w, int slot) {
     sg.store(w, lq, ld);
     __syncthreads();
     const uint32_t nb = min(kGStageBlocks, kblocks - s * kGStageBlocks);
@@ -400,9 +419,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
     for (int j = 0; j < kGWaveBlocks; ++j) {
       const uint32_t b = wave + 4 * j;
       if (b >= nb) break;  // uniform
+      const float bsj = bok[slot][j] ? bs[slot][j] : 0.f;
       long bk[3];
 #pragma unroll
-      for (int k = 0; k < 3; ++k) bk[k] = (long)(((uint64_t)bv[j][k].y << 32) | bv[j][k].x);
+      for (int k = 0; k < 3; ++k) bk[k] = (long)(((uint64_t)bv[slot][j][k].y << 32) | bv[slot][j][k].x);
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
         const long av = *reinterpret_cast<const long *>(lq + (a * 16 + col) * kGRowStride + b * 32 + kg * 8);
@@ -416,21 +436,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
         for (int i = 0; i < 4; ++i) {
           const float hi = (float)(p1[i] + (p2[i] << 8));
           const float v = __builtin_fmaf(hi, 256.0f, (float)p0[i]);
-          acc[a][i] = __builtin_fmaf(v, dd[i] * bs[j], acc[a][i]);
+          acc[a][i] = __builtin_fmaf(v, dd[i] * bsj, acc[a][i]);
         }
       }
     }
-    // Next stage's B operands first, then the weight refill of stage s + 2:
-    // loads retire in issue order, so stage s + 1's MFMAs, which wait for
-    // the B operands, then do not also wait for stage s + 2's weights, and
-    // two weight stages stay in flight.
-    if (s + 1 < n_stages) load_b(s + 1);
-    if (s + 2 < n_stages) sg.load(s + 2, row_chunks, FUSED, w);
-    __syncthreads();  // LDS slab consumed before the next store
   };
-  for (uint32_t s = 0; s < n_stages; s += 2) {
-    stage(s, wbuf[0]);
-    if (s + 1 < n_stages) stage(s + 1, wbuf[1]);
+  // The weight refill is issued on every round (a stage past the last reads
+  // zeros without touching memory), so each buffer is redefined on every
+  // path and stays in its registers; the B operands past the last stage are
+  // skipped, as they would be real reads.
+  for (uint32_t s = 0; s < n_stages; s += kGInFlight) {
+#pragma unroll
+    for (int b = 0; b < kGInFlight; ++b) {
+      if (s + b < n_stages) stage(s + b, wbuf[b], b);  // uniform
+      if (s + b + kGInFlight < n_stages) load_b(s + b + kGInFlight, b);
+      sg.load(s + b + kGInFlight, row_chunks, wbuf[b]);
+      __syncthreads();  // LDS slab consumed before the next store
+    }
   }
 
   // sum the four waves' partials (in the slab's LDS, free now); wave w
