@@ -782,12 +782,10 @@ int run_grouped(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_token
   const size_t n_plist = up64(p.n_pairs);
   const size_t n_ok = up64(p.n_pairs);
   const size_t n_tiles = up64((size_t)max_tiles * sizeof(GroupTile) / 4);
-  const size_t n_xg = up64((size_t)n_tokens * p.xblocks * 24);
-  const size_t n_xs = up64((size_t)n_tokens * p.xblocks);
-  const size_t n_hg = up64((size_t)p.n_pairs * p.hblocks * 24);
-  const size_t n_hs = up64((size_t)p.n_pairs * p.hblocks);
+  const size_t n_xg = up64((size_t)n_tokens * p.xblocks * 32);  // 4 k-group records of 8 dwords per block
+  const size_t n_hg = up64((size_t)p.n_pairs * p.hblocks * 32);
   const size_t n_pa = up64((size_t)p.n_pairs * dm);
-  const size_t total = n_hdr + n_plist + n_ok + n_tiles + n_xg + n_xs + n_hg + n_hs + n_pa;
+  const size_t total = n_hdr + n_plist + n_ok + n_tiles + n_xg + n_hg + n_pa;
   float *cur = nullptr;
   int rc = ensure_scratch(w, total, &cur);
   if (rc) return rc;
@@ -801,12 +799,8 @@ int run_grouped(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_token
   cur += n_tiles;
   p.xg = reinterpret_cast<uint32_t *>(cur);
   cur += n_xg;
-  p.xs = cur;
-  cur += n_xs;
   p.hg = reinterpret_cast<uint32_t *>(cur);
   cur += n_hg;
-  p.hs = cur;
-  cur += n_hs;
   p.partial = cur;
 
   const int fmt = fmt_of(dtype);

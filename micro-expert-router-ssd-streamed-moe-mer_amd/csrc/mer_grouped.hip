@@ -40,8 +40,9 @@
 // 4 (l / 16) + i, i = 0..3, of column l % 16.  Weights are staged through
 // LDS as [row][block][32 int8] (rows padded to spread banks) plus f32
 // scales [block][row]; the input digits are stored per (vector, block) as
-// 4 groups x {8 bytes v0, 8 bytes v1, 8 bytes v2}, so a lane reads the B
-// operands of its k-group from one 24-byte record.
+// 4 groups x {8 bytes v0, 8 bytes v1, 8 bytes v2, f32 scale, pad}, so a
+// lane reads the B operands of its k-group and the block scale from one
+// 32-byte record.
 #include "mer_internal.hpp"
 
 namespace mer {
@@ -72,7 +73,7 @@ constexpr uint32_t kGRowStride = kGStageBlocks * 32 + 16;  // LDS bytes per stag
 // threads that stage consecutive rows' chunks write different banks.
 constexpr uint32_t kGScaleStride = kGRows + 4;
 constexpr float kGIntMax = 8355711.0f;   // |v| bound (0x7f7f7f): v + 0x808080 stays in 24 bits
-constexpr uint32_t kGRec = 6;            // dwords per (vector, block, k-group) digit record
+constexpr uint32_t kGRec = 8;            // dwords per (vector, block, k-group) record: 3 digit planes, scale, pad
 constexpr uint32_t kNoChunkG = 0x80000000u;
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
@@ -89,10 +90,11 @@ __device__ __forceinline__ bool pair_valid(const GroupedParams &p, uint32_t pair
 }
 
 // Quantise 8 elements (one MFMA k-group) of a block whose 4 groups sit in
-// 4 adjacent lanes (lane & 3 = group): block max by shuffles, then the three
-// digit planes as one 24-byte record {v0[8], v1[8], v2[8]}.
-// Only lanes with `store` write; the group's first lane writes the scale.
-__device__ __forceinline__ void quant_group(const float (&v)[8], uint32_t *dst, float *scale, bool lead, bool store) {
+// 4 adjacent lanes (lane & 3 = group): block max by shuffles, then one
+// 32-byte record {v0[8], v1[8], v2[8], f32 block scale, 0}, so a reader
+// gets a k-group's three digit planes and the block's scale with two
+// 16-byte loads.  Only lanes with `store` write.
+__device__ __forceinline__ void quant_group(const float (&v)[8], uint32_t *dst, bool store) {
   float amax = 0.f;
   int finite = 1;
 #pragma unroll
@@ -116,7 +118,7 @@ __device__ __forceinline__ void quant_group(const float (&v)[8], uint32_t *dst, 
     s = amax / kGIntMax;
     inv = kGIntMax / amax;
   }
-  uint32_t d[kGRec] = {0u, 0u, 0u, 0u, 0u, 0u};
+  uint32_t d[6] = {0u, 0u, 0u, 0u, 0u, 0u};
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     float q = __builtin_rintf(v[i] * inv);
@@ -126,11 +128,9 @@ __device__ __forceinline__ void quant_group(const float (&v)[8], uint32_t *dst, 
     for (int k = 0; k < 3; ++k) d[2 * k + (i >> 2)] |= ((u >> (8 * k)) & 0xffu) << (8 * (i & 3));
   }
   if (!store) return;
-  uint2 *o = reinterpret_cast<uint2 *>(dst);
-  o[0] = make_uint2(d[0], d[1]);
-  o[1] = make_uint2(d[2], d[3]);
-  o[2] = make_uint2(d[4], d[5]);
-  if (lead) *scale = s;
+  uint4 *o = reinterpret_cast<uint4 *>(dst);
+  o[0] = make_uint4(d[0], d[1], d[2], d[3]);
+  o[1] = make_uint4(d[4], d[5], __float_as_uint(s), 0u);
 }
 
 // Block 0: group the routed pairs by expert.  Other blocks: quantise x.
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(1024) void group_kernel(GroupedParams p) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = 0.f;
     }
-    quant_group(v, p.xg + ((size_t)tb * 4 + m) * kGRec, p.xs + tb, m == 0, valid);
+    quant_group(v, p.xg + ((size_t)tb * 4 + m) * kGRec, valid);
     return;
   }
 
@@ -365,16 +365,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerE
   const uint32_t col = lane % 16, kg = lane / 16;
   const uint32_t pair = s_pair[col];
   const bool col_ok = pair != 0xffffffffu;
-  const uint2 *vdig;  // the lane's record of block 0; block b is 4 * kGRec / 2 uint2 further
-  const float *vsc;
+  const uint4 *vrec;  // the lane's record of block 0; block b's is 4 records (8 uint4) further
   if constexpr (FUSED) {
     const uint32_t t = col_ok ? pair / p.top_k : 0;
-    vdig = reinterpret_cast<const uint2 *>(p.xg + ((size_t)t * p.xblocks * 4 + kg) * kGRec);
-    vsc = p.xs + (size_t)t * p.xblocks;
+    vrec = reinterpret_cast<const uint4 *>(p.xg + ((size_t)t * p.xblocks * 4 + kg) * kGRec);
   } else {
     const uint32_t pr = col_ok ? pair : 0;
-    vdig = reinterpret_cast<const uint2 *>(p.hg + ((size_t)pr * p.hblocks * 4 + kg) * kGRec);
-    vsc = p.hs + (size_t)pr * p.hblocks;
+    vrec = reinterpret_cast<const uint4 *>(p.hg + ((size_t)pr * p.hblocks * 4 + kg) * kGRec);
   }
 
   float acc[4][4];
@@ -398,9 +395,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerE
       const uint32_t b = wave + 4 * j;
       bok[slot][j] = col_ok && b < left;
       const uint32_t gb = bok[slot][j] ? s * kGStageBlocks + b : 0u;
-#pragma unroll
-      for (int k = 0; k < 3; ++k) bv[slot][j][k] = vdig[(size_t)gb * 2 * kGRec + k];
-      bs[slot][j] = vsc[gb];
+      const uint4 r0 = vrec[(size_t)gb * 8], r1 = vrec[(size_t)gb * 8 + 1];
+      bv[slot][j][0] = make_uint2(r0.x, r0.y);
+      bv[slot][j][1] = make_uint2(r0.z, r0.w);
+      bv[slot][j][2] = make_uint2(r1.x, r1.y);
+      bs[slot][j] = __uint_as_float(r1.z);
     }
   };
   // Issue order B(0), W(0), B(1), W(1), ...: the order in which the loop
@@ -496,7 +495,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerE
       const uint32_t pr = s_pair[c];
       const bool ok = pr != 0xffffffffu;
       const size_t hb = (size_t)(ok ? pr : 0) * p.hblocks + rt;
-      quant_group(h, p.hg + (hb * 4 + m) * kGRec, p.hs + hb, m == 0, ok);
+      quant_group(h, p.hg + (hb * 4 + m) * kGRec, ok);
     }
   } else {
     if (col_ok) {

@@ -166,10 +166,8 @@ struct GroupedParams {
   float swiglu_limit;        // gate clamp before SiLU (+inf = none)
   size_t proj_bytes;
   // scratch
-  uint32_t *xg;              // x digits [n_tok][xblocks][4 k-groups][6 dwords]
-  float *xs;                 // x block scales [n_tok][xblocks]
-  uint32_t *hg;              // h digits [n_pairs][hblocks][4][6 dwords]
-  float *hs;                 // h block scales [n_pairs][hblocks]
+  uint32_t *xg;              // x digit records [n_tok][xblocks][4 k-groups][8 dwords]
+  uint32_t *hg;              // h digit records [n_pairs][hblocks][4][8 dwords]
   float *partial;            // w_i y_i [n_pairs][d_model]
   uint32_t *plist;           // pairs grouped by expert [n_pairs]
   uint32_t *pair_ok;         // [n_pairs] 1 = routed to a resident expert with a nonzero weight
