@@ -58,12 +58,6 @@ constexpr uint32_t kGRows = 64;          // weight rows staged per workgroup
 // stages with one in flight (measured on the 64-token Qwen3 batch: down
 // 39 -> 36 us, 493K -> 508K tokens/s; gate/up unchanged).
 constexpr uint32_t kGStageBlocks = 8;
-#ifndef MER_G_INFLIGHT_GU
-#define MER_G_INFLIGHT_GU 2
-#endif
-#ifndef MER_G_INFLIGHT_DN
-#define MER_G_INFLIGHT_DN 2
-#endif
 constexpr int kGWavesPerEu = 4;
 constexpr uint32_t kGStageChunks = kGStageBlocks / 2;  // two-block chunks per row per stage
 constexpr int kGChunksPerThread = (int)(kGRows * kGStageChunks / 256);
@@ -333,9 +327,12 @@ struct Stager {
 // down rows; the epilogue writes w_i * y_i per pair.
 template <int FMT, bool FUSED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerEu))) void gproj_kernel(GroupedParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lq[kGRows * kGRowStride];
-  __shared__ __attribute__((aligned(16))) float ld[kGStageBlocks * kGScaleStride];
+  // Two LDS slabs: stage s + 1 is stored into one while stage s is read
+  // from the other, so a stage needs one barrier.
+  __shared__ __attribute__((aligned(16))) uint8_t lq_buf[2][kGRows * kGRowStride];
+  __shared__ __attribute__((aligned(16))) float ld_buf[2][kGStageBlocks * kGScaleStride];
   __shared__ uint32_t s_pair[kGTok];
+  uint8_t *const lq = lq_buf[0];
 
   const uint32_t row_tiles = FUSED ? p.d_ff / 32 : p.d_model / kGRows;
   const uint32_t tile = blockIdx.x / row_tiles;
@@ -355,10 +352,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerE
     sg.init(gt.blob + 2 * p.proj_bytes + (size_t)rt * kGRows * row_bytes, 0u, row_bytes, false);
   }
   const uint32_t n_stages = (kblocks + kGStageBlocks - 1) / kGStageBlocks;
-  // kGInFlight stages in flight: stage s + kGInFlight loads into the buffer
-  constexpr int kGInFlight = FUSED ? MER_G_INFLIGHT_GU : MER_G_INFLIGHT_DN;
-  // stage s leaves.
-  typename Stager<FMT>::Buf wbuf[kGInFlight];
+  // Two register buffers of weight loads: W(s) lives in wbuf[s & 1].
+  typename Stager<FMT>::Buf wbuf[2];
   __syncthreads();  // s_pair
 
   // B operands: the lane's column is pair s_pair[lane % 16]; its k-group is lane / 16
@@ -380,14 +375,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerE
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[a][i] = 0.f;
 
-  // B operands of this wave's blocks of stage s (wave, wave + 4, ...), in
-  // a ring of kGInFlight slots loaded as far ahead as the weights: stage
-  // s + kGInFlight's B operands are issued right after stage s's MFMAs,
-  // just before its weight refill.  A lane without a valid block reads
-  // block 0 of its record and gets a zero scale.
-  uint2 bv[kGInFlight][kGWaveBlocks][3];
-  float bs[kGInFlight][kGWaveBlocks];
-  bool bok[kGInFlight][kGWaveBlocks];
+  // B operands of this wave's blocks of stage s (wave, wave + 4, ...) live
+  // in slot s & 1.  A lane without a valid block (or a stage past the last)
+  // reads block 0 of its record and gets a zero scale.
+  uint2 bv[2][kGWaveBlocks][3];
+  float bs[2][kGWaveBlocks];
+  bool bok[2][kGWaveBlocks];
   auto load_b = [&](uint32_t s, int slot) {
     const uint32_t left = s < n_stages ? kblocks - s * kGStageBlocks : 0u;
 #pragma unroll
@@ -395,24 +388,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerE
       const uint32_t b = wave + 4 * j;
       bok[slot][j] = col_ok && b < left;
       const uint32_t gb = bok[slot][j] ? s * kGStageBlocks + b : 0u;
-      const uint4 r0 = vrec[(size_t)gb * 8], r1 = vrec[(size_t)gb * 8 + 1];
+      const uint4 *rp = vrec + gb * 8u;
+      const uint4 r0 = rp[0], r1 = rp[1];
       bv[slot][j][0] = make_uint2(r0.x, r0.y);
       bv[slot][j][1] = make_uint2(r0.z, r0.w);
       bv[slot][j][2] = make_uint2(r1.x, r1.y);
       bs[slot][j] = __uint_as_float(r1.z);
     }
   };
-  // Issue order B(0), W(0), B(1), W(1), ...: the order in which the loop
-  // below leaves each stage's loads outstanding, so the wait counts are the
-  // same on the first round as on every later one.
-#pragma unroll
-  for (int b = 0; b < kGInFlight; ++b) {
-    load_b(b, b);
-    sg.load(b, row_chunks, wbuf[b]);
-  }
-  auto stage = [&](uint32_t s, typename Stager<FMT>::Buf &w, int slot) {
-    sg.store(w, lq, ld);
-    __syncthreads();
+  // Loads and slabs alternate between two buffers: at round s the wave
+  // issues B(s + 1) and W(s + 2), stores W(s + 1) into the slab stage s
+  // does not read, computes stage s and meets the others at the barrier.
+  // Every load and store is issued unconditionally (weights past the last
+  // stage read zeros without touching memory; B operands past it re-read
+  // block 0), so each register buffer is redefined on every path: no
+  // branch merges two versions of a buffer, which the compiler would
+  // resolve with copies that wait for the loads just issued.  The prologue
+  // leaves the loads outstanding in the loop's order (W(s + 1) older than
+  // B(s + 1), W(s + 2)), so the wait counts are the same on the first round
+  // as on every later one.  (Measured, config 3 gate/up: one slab with two
+  // barriers per stage 69 us, two slabs 61-63 us.)
+  sg.load(0, row_chunks, wbuf[0]);
+  load_b(0, 0);
+  sg.load(1, row_chunks, wbuf[1]);
+  sg.store(wbuf[0], lq_buf[0], ld_buf[0]);
+  __syncthreads();
+  auto stage = [&](uint32_t s, int slot) {
+    const uint8_t *sl = lq_buf[slot];
+    const float *sd = ld_buf[slot];
     const uint32_t nb = min(kGStageBlocks, kblocks - s * kGStageBlocks);
 #pragma unroll
     for (int j = 0; j < kGWaveBlocks; ++j) {
@@ -424,12 +427,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerE
       for (int k = 0; k < 3; ++k) bk[k] = (long)(((uint64_t)bv[slot][j][k].y << 32) | bv[slot][j][k].x);
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        const long av = *reinterpret_cast<const long *>(lq + (a * 16 + col) * kGRowStride + b * 32 + kg * 8);
+        const long av = *reinterpret_cast<const long *>(sl + (a * 16 + col) * kGRowStride + b * 32 + kg * 8);
         const v4i z = {0, 0, 0, 0};
         const v4i p0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[0], z, 0, 0, 0);
         const v4i p1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[1], z, 0, 0, 0);
         const v4i p2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[2], z, 0, 0, 0);
-        const float4 d = *reinterpret_cast<const float4 *>(&ld[b * kGScaleStride + a * 16 + kg * 4]);
+        const float4 d = *reinterpret_cast<const float4 *>(&sd[b * kGScaleStride + a * 16 + kg * 4]);
         const float dd[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -440,17 +443,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerE
       }
     }
   };
-  // The weight refill is issued on every round (a stage past the last reads
-  // zeros without touching memory), so each buffer is redefined on every
-  // path and stays in its registers; the B operands past the last stage are
-  // skipped, as they would be real reads.
-  for (uint32_t s = 0; s < n_stages; s += kGInFlight) {
+  for (uint32_t s = 0; s < n_stages; s += 2) {
 #pragma unroll
-    for (int b = 0; b < kGInFlight; ++b) {
-      if (s + b < n_stages) stage(s + b, wbuf[b], b);  // uniform
-      if (s + b + kGInFlight < n_stages) load_b(s + b + kGInFlight, b);
-      sg.load(s + b + kGInFlight, row_chunks, wbuf[b]);
-      __syncthreads();  // LDS slab consumed before the next store
+    for (int b = 0; b < 2; ++b) {
+      const uint32_t st = s + b;
+      load_b(st + 1, b ^ 1);
+      sg.load(st + 2, row_chunks, wbuf[b]);
+      sg.store(wbuf[b ^ 1], lq_buf[b ^ 1], ld_buf[b ^ 1]);
+      if (st < n_stages) stage(st, b);  // uniform
+      __syncthreads();
     }
   }
 
