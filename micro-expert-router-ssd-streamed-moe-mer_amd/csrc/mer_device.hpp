@@ -205,29 +205,38 @@ __device__ __forceinline__ void pack_group(const float *v, float inv, uint32_t *
 template <int FMT>
 __device__ __forceinline__ float block_idot(const uint32_t *q, const uint32_t *dig) {
   if constexpr (FMT == FMT_Q4_0) {
-    int a[6];
+    // Horner over the base-16 planes inside the dot chains: each plane's
+    // dots accumulate onto the running sum shifted by 4, so a block needs
+    // two zeroed accumulators instead of six.  |plane sum| <= 2048, so
+    // planes 0-3 (lo) stay below 2^24 and planes 4-5 (hi) below 2^16.
+    uint32_t qs[4];
 #pragma unroll
-    for (int k = 0; k < 6; ++k) {
-      a[k] = 0;
+    for (int m = 0; m < 4; ++m) qs[m] = q[m] ^ 0x88888888u;
+    int lo = 0, hi = 0;
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
-        a[k] = __builtin_amdgcn_sdot8((int)(q[m] ^ 0x88888888u), (int)dig[k * 4 + m], a[k], false);
+    for (int k = 3; k >= 0; --k) {
+      if (k < 3) lo <<= 4;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) lo = __builtin_amdgcn_sdot8((int)qs[m], (int)dig[k * 4 + m], lo, false);
     }
-    // |a_k| <= 2048: pairwise base-16 sums fit easily; p0 + 256*p1 < 2^24
-    const int p0 = a[0] + (a[1] << 4);
-    const int p1 = a[2] + (a[3] << 4);
-    const int p2 = a[4] + (a[5] << 4);
-    const int lo = p0 + (p1 << 8);
-    return __builtin_fmaf((float)p2, 65536.0f, (float)lo);
+#pragma unroll
+    for (int k = 5; k >= 4; --k) {
+      if (k < 5) hi <<= 4;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) hi = __builtin_amdgcn_sdot8((int)qs[m], (int)dig[k * 4 + m], hi, false);
+    }
+    return __builtin_fmaf((float)hi, 65536.0f, (float)lo);
   } else {
-    int a[3];
+    // planes 0-1 (|sum| < 2^27) in one chain, plane 2 in another
+    int lo = 0, hi = 0;
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      a[k] = 0;
+    for (int m = 0; m < 8; ++m) lo = __builtin_amdgcn_sdot4((int)q[m], (int)dig[8 + m], lo, false);
+    lo <<= 8;
 #pragma unroll
-      for (int m = 0; m < 8; ++m) a[k] = __builtin_amdgcn_sdot4((int)q[m], (int)dig[k * 8 + m], a[k], false);
-    }
-    return __builtin_fmaf((float)a[2], 65536.0f, __builtin_fmaf((float)a[1], 256.0f, (float)a[0]));
+    for (int m = 0; m < 8; ++m) lo = __builtin_amdgcn_sdot4((int)q[m], (int)dig[m], lo, false);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) hi = __builtin_amdgcn_sdot4((int)q[m], (int)dig[16 + m], hi, false);
+    return __builtin_fmaf((float)hi, 65536.0f, (float)lo);
   }
 }
 
