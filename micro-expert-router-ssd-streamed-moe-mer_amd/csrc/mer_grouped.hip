@@ -52,20 +52,26 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kGTok = 16;           // pairs per token tile (MFMA N)
-constexpr uint32_t kGRows = 64;          // weight rows staged per workgroup
-// K blocks per LDS stage.  Eight-block stages with two in flight per
-// workgroup (one two-block chunk per thread and stage) beat sixteen-block
-// stages with one in flight (measured on the 64-token Qwen3 batch: down
-// 39 -> 36 us, 493K -> 508K tokens/s; gate/up unchanged).
-constexpr uint32_t kGStageBlocks = 8;
 constexpr int kGWavesPerEu = 4;
-constexpr uint32_t kGStageChunks = kGStageBlocks / 2;  // two-block chunks per row per stage
-constexpr int kGChunksPerThread = (int)(kGRows * kGStageChunks / 256);
-constexpr int kGWaveBlocks = (int)(kGStageBlocks / 4);  // blocks of a stage per wave
-constexpr uint32_t kGRowStride = kGStageBlocks * 32 + 16;  // LDS bytes per staged row
-// Scales are stored [block][row] with a padded row of 68 floats, so the
-// threads that stage consecutive rows' chunks write different banks.
-constexpr uint32_t kGScaleStride = kGRows + 4;
+// Workgroup geometry: four waves, RT row tiles of 16 rows (RT = 4 or 8),
+// stages of 32 / RT blocks, so every stage holds the same 256 two-block
+// chunks (one per thread) whatever RT is.  Each wave computes every row
+// tile for its 32 / (4 RT) blocks of the stage: with RT = 8 a B operand
+// (one pair column's digit records of one block) serves twice as many
+// weight rows, which halves the B bytes loaded per weight byte.
+template <int RT>
+struct GGeom {
+  static constexpr uint32_t kRows = 16 * RT;                       // weight rows per workgroup
+  static constexpr uint32_t kStageBlocks = 32 / RT;                // K blocks per stage
+  static constexpr uint32_t kStageChunks = kStageBlocks / 2;       // two-block chunks per row per stage
+  static constexpr int kWaveBlocks = (int)(kStageBlocks / 4);      // blocks of a stage per wave
+  static constexpr uint32_t kRowStride = kStageBlocks * 32 + 16;   // LDS bytes per staged row (padded)
+  // scales [block][row]; RT = 4 pads the row to spread the stores' banks,
+  // RT = 8 keeps two slabs within a quarter of the CU's LDS
+  static constexpr uint32_t kScaleStride = RT == 4 ? kRows + 4 : kRows;
+  static_assert(kRows * kStageChunks == 256, "one chunk per thread and stage");
+  static_assert(kWaveBlocks >= 1, "every wave has a block in every stage");
+};
 constexpr float kGIntMax = 8355711.0f;   // |v| bound (0x7f7f7f): v + 0x808080 stays in 24 bits
 constexpr uint32_t kGRec = 8;            // dwords per (vector, block, k-group) record: 3 digit planes, scale, pad
 constexpr uint32_t kNoChunkG = 0x80000000u;
@@ -227,167 +233,169 @@ __global__ __launch_bounds__(1024) void group_kernel(GroupedParams p) {
     if (pos[q] != 0xffffffffu) p.plist[cnt[p.ids[q]] + pos[q]] = q;
 }
 
-// Stage one 64-row x kGStageBlocks-block slab of weights into LDS: two-block
-// chunks, kGChunksPerThread per thread, loaded with raw buffer loads into a
-// register buffer (a chunk past the row's end reads zeros) and stored as
-// int8 rows plus f32 scales.
-template <int FMT>
+// Stage one (16 RT)-row x (32 / RT)-block slab of weights into LDS: one
+// two-block chunk per thread, loaded with raw buffer loads into a register
+// buffer (a chunk past the row's end reads zeros) and stored as int8 rows
+// plus f32 scales.
+template <int FMT, int RT>
 struct Stager {
+  using Geo = GGeom<RT>;
   using T = FmtTraits<FMT>;
   static constexpr int kDw = T::kChunkDwords;
   __amdgpu_buffer_rsrc_t rsrc;           // one descriptor for the whole slab (uniform, so no per-lane waterfall)
-  uint32_t voff[kGChunksPerThread];      // byte offset of this thread's chunk c (stage 0)
-  uint32_t schunk[kGChunksPerThread];
-  uint32_t srow[kGChunksPerThread];
-  using Buf = uint32_t[kGChunksPerThread][kDw];
+  uint32_t voff;      // byte offset of this thread's chunk (stage 0)
+  uint32_t schunk;
+  uint32_t srow;
+  using Buf = uint32_t[kDw];
 
-  // fused: slab rows 0..31 are gate rows starting at base, rows 32..63 the
-  // same up rows, up_off bytes further; otherwise 64 consecutive rows.
+  // fused: slab rows 0 .. 8 RT - 1 are gate rows starting at base, the
+  // next 8 RT the same up rows, up_off bytes further; otherwise 16 RT
+  // consecutive rows.
   __device__ __forceinline__ void init(const uint8_t *base, uint32_t up_off, uint32_t row_bytes, bool fused) {
     rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, 0x7fffffff, 0x00020000);
-#pragma unroll
-    for (int i = 0; i < kGChunksPerThread; ++i) {
-      const uint32_t c = threadIdx.x + 256u * i;  // chunk of the slab: row c / kGStageChunks
-      srow[i] = c / kGStageChunks;
-      schunk[i] = c % kGStageChunks;
-      const bool up = fused && srow[i] >= 32;
-      const uint32_t r = up ? srow[i] - 32 : srow[i];
-      voff[i] = (up ? up_off : 0u) + r * row_bytes + schunk[i] * (uint32_t)T::kChunkBytes;
-    }
+    const uint32_t c = threadIdx.x;  // chunk of the slab: row c / kStageChunks
+    srow = c / Geo::kStageChunks;
+    schunk = c % Geo::kStageChunks;
+    const bool up = fused && srow >= Geo::kRows / 2;
+    const uint32_t r = up ? srow - Geo::kRows / 2 : srow;
+    voff = (up ? up_off : 0u) + r * row_bytes + schunk * (uint32_t)T::kChunkBytes;
   }
 
-  // Issue the loads of stage s (its kGStageChunks chunks of each row) into
+  // Issue the loads of stage s (its kStageChunks chunks of each row) into
   // w.  Chunks past the row's end (and every chunk of a stage past the
   // last) read zeros, so the loads are issued unconditionally: w is
   // redefined on every path, which keeps the register buffers in place
   // instead of merging two versions of them after a branch.
   __device__ __forceinline__ void load(uint32_t s, uint32_t row_chunks, Buf &w) const {
+    const bool ok = s * Geo::kStageChunks + schunk < row_chunks;
+    const uint32_t off = ok ? voff + s * Geo::kStageChunks * (uint32_t)T::kChunkBytes : kNoChunkG;
 #pragma unroll
-    for (int i = 0; i < kGChunksPerThread; ++i) {
-      const bool ok = s * kGStageChunks + schunk[i] < row_chunks;
-      const uint32_t off = ok ? voff[i] + s * kGStageChunks * (uint32_t)T::kChunkBytes : kNoChunkG;
-#pragma unroll
-      for (int v = 0; v < kDw / 4; ++v) {
-        const uint4 q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off + 16 * v, 0, 0));
-        w[i][4 * v] = q.x;
-        w[i][4 * v + 1] = q.y;
-        w[i][4 * v + 2] = q.z;
-        w[i][4 * v + 3] = q.w;
-      }
-      w[i][kDw - 1] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, off + 16 * (kDw / 4), 0, 0);
+    for (int v = 0; v < kDw / 4; ++v) {
+      const uint4 q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off + 16 * v, 0, 0));
+      w[4 * v] = q.x;
+      w[4 * v + 1] = q.y;
+      w[4 * v + 2] = q.z;
+      w[4 * v + 3] = q.w;
     }
+    w[kDw - 1] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, off + 16 * (kDw / 4), 0, 0);
   }
 
   // Write the loaded chunks to LDS: q as int8 [row][block][32], scales
   // as f32 [block][row].
   __device__ __forceinline__ void store(const Buf &w, uint8_t *lq, float *ld) const {
-#pragma unroll
-    for (int i = 0; i < kGChunksPerThread; ++i) {
+    {
       uint32_t q0[8], q1[8];
       float d0, d1;
       if constexpr (FMT == FMT_Q4_0) {
         // block 0: d = w0[15:0], qs = bytes 2..17; block 1: d = w4[31:16], qs = w5..w8
-        const uint32_t a[4] = {realign16(w[i][0], w[i][1]), realign16(w[i][1], w[i][2]), realign16(w[i][2], w[i][3]),
-                               realign16(w[i][3], w[i][4])};
+        const uint32_t a[4] = {realign16(w[0], w[1]), realign16(w[1], w[2]), realign16(w[2], w[3]),
+                               realign16(w[3], w[4])};
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           // element j = low nibble of qs[j], j + 16 = high nibble; int8 q - 8
           q0[m] = ((a[m] & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
           q0[4 + m] = (((a[m] >> 4) & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
-          const uint32_t b = w[i][5 + m];
+          const uint32_t b = w[5 + m];
           q1[m] = ((b & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
           q1[4 + m] = (((b >> 4) & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
         }
-        d0 = f16_bits_to_f32(w[i][0] & 0xffffu);
-        d1 = f16_bits_to_f32(w[i][4] >> 16);
+        d0 = f16_bits_to_f32(w[0] & 0xffffu);
+        d1 = f16_bits_to_f32(w[4] >> 16);
       } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-          q0[k] = realign16(w[i][k], w[i][k + 1]);
-          q1[k] = w[i][9 + k];
+          q0[k] = realign16(w[k], w[k + 1]);
+          q1[k] = w[9 + k];
         }
-        d0 = f16_bits_to_f32(w[i][0] & 0xffffu);
-        d1 = f16_bits_to_f32(w[i][8] >> 16);
+        d0 = f16_bits_to_f32(w[0] & 0xffffu);
+        d1 = f16_bits_to_f32(w[8] >> 16);
       }
-      const uint32_t b0 = 2 * schunk[i];
-      uint4 *dst = reinterpret_cast<uint4 *>(lq + srow[i] * kGRowStride + b0 * 32);
+      const uint32_t b0 = 2 * schunk;
+      uint4 *dst = reinterpret_cast<uint4 *>(lq + srow * Geo::kRowStride + b0 * 32);
       dst[0] = make_uint4(q0[0], q0[1], q0[2], q0[3]);
       dst[1] = make_uint4(q0[4], q0[5], q0[6], q0[7]);
       dst[2] = make_uint4(q1[0], q1[1], q1[2], q1[3]);
       dst[3] = make_uint4(q1[4], q1[5], q1[6], q1[7]);
-      ld[b0 * kGScaleStride + srow[i]] = d0;
-      ld[(b0 + 1) * kGScaleStride + srow[i]] = d1;
+      ld[b0 * Geo::kScaleStride + srow] = d0;
+      ld[(b0 + 1) * Geo::kScaleStride + srow] = d1;
     }
   }
 };
 
-// One workgroup (4 waves) per (token tile, 64 staged rows).  FUSED: rows
-// 0..31 are gate rows r0.., rows 32..63 the same up rows; the epilogue
-// writes h = silu(g) * u for 32 rows = one block per pair.  Otherwise 64
-// down rows; the epilogue writes w_i * y_i per pair.
-template <int FMT, bool FUSED>
+// One workgroup (4 waves) per (token tile, 16 RT staged rows).  FUSED:
+// rows 0 .. 8 RT - 1 are gate rows, the next 8 RT the same up rows; the
+// epilogue writes h = silu(g) * u for 8 RT rows = RT / 4 blocks per pair.
+// Otherwise 16 RT down rows; the epilogue writes w_i * y_i per pair.
+template <int FMT, bool FUSED, int RT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerEu))) void gproj_kernel(GroupedParams p) {
+  using Geo = GGeom<RT>;
+  using SG = Stager<FMT, RT>;
+  constexpr uint32_t kRows = Geo::kRows, kSB = Geo::kStageBlocks, kStride = Geo::kRowStride, kSS = Geo::kScaleStride;
+  constexpr int kWB = Geo::kWaveBlocks;
   // Two LDS slabs: stage s + 1 is stored into one while stage s is read
   // from the other, so a stage needs one barrier.
-  __shared__ __attribute__((aligned(16))) uint8_t lq_buf[2][kGRows * kGRowStride];
-  __shared__ __attribute__((aligned(16))) float ld_buf[2][kGStageBlocks * kGScaleStride];
-  __shared__ uint32_t s_pair[kGTok];
+  __shared__ __attribute__((aligned(16))) uint8_t lq_buf[2][kRows * kStride];
+  __shared__ __attribute__((aligned(16))) float ld_buf[2][kSB * kSS];
   uint8_t *const lq = lq_buf[0];
 
-  const uint32_t row_tiles = FUSED ? p.d_ff / 32 : p.d_model / kGRows;
+  const uint32_t row_tiles = FUSED ? p.d_ff / (kRows / 2) : p.d_model / kRows;
   const uint32_t tile = blockIdx.x / row_tiles;
   const uint32_t rt = blockIdx.x % row_tiles;
   if (tile >= *p.n_tiles) return;  // uniform over the workgroup
   const GroupTile gt = p.tiles[tile];
   const uint32_t tid = threadIdx.x, lane = lane_id(), wave = tid / 64u;
-  if (tid < kGTok) s_pair[tid] = tid < gt.count ? p.plist[gt.start + tid] : 0xffffffffu;
+  // B operands: the lane's column is the tile's pair lane % 16; its k-group
+  // is lane / 16.  Every lane reads its column's pair index (16 words per
+  // wave) before the weights are issued: loads complete in issue order, so
+  // the B addresses never wait for weights.
+  const uint32_t col = lane % 16, kg = lane / 16;
+  const uint32_t pair = col < gt.count ? p.plist[gt.start + col] : 0xffffffffu;
+  const bool col_ok = pair != 0xffffffffu;
 
   const uint32_t kblocks = FUSED ? p.xblocks : p.hblocks;  // K / 32
   const uint32_t row_chunks = kblocks / 2;
   const uint32_t row_bytes = kblocks * (uint32_t)FmtTraits<FMT>::kBlockBytes;
-  Stager<FMT> sg;
+  SG sg;
   if constexpr (FUSED) {
-    sg.init(gt.blob + (size_t)rt * 32 * row_bytes, (uint32_t)p.proj_bytes, row_bytes, true);
+    sg.init(gt.blob + (size_t)rt * (kRows / 2) * row_bytes, (uint32_t)p.proj_bytes, row_bytes, true);
   } else {
-    sg.init(gt.blob + 2 * p.proj_bytes + (size_t)rt * kGRows * row_bytes, 0u, row_bytes, false);
+    sg.init(gt.blob + 2 * p.proj_bytes + (size_t)rt * kRows * row_bytes, 0u, row_bytes, false);
   }
-  const uint32_t n_stages = (kblocks + kGStageBlocks - 1) / kGStageBlocks;
+  const uint32_t n_stages = (kblocks + kSB - 1) / kSB;
   // Two register buffers of weight loads: W(s) lives in wbuf[s & 1].
-  typename Stager<FMT>::Buf wbuf[2];
-  __syncthreads();  // s_pair
+  typename SG::Buf wbuf[2];
+  sg.load(0, row_chunks, wbuf[0]);
+  sg.load(1, row_chunks, wbuf[1]);
+  __builtin_amdgcn_sched_barrier(0);  // the weights go out before anything waits for the pair index
 
-  // B operands: the lane's column is pair s_pair[lane % 16]; its k-group is lane / 16
-  const uint32_t col = lane % 16, kg = lane / 16;
-  const uint32_t pair = s_pair[col];
-  const bool col_ok = pair != 0xffffffffu;
-  const uint4 *vrec;  // the lane's record of block 0; block b's is 4 records (8 uint4) further
-  if constexpr (FUSED) {
-    const uint32_t t = col_ok ? pair / p.top_k : 0;
-    vrec = reinterpret_cast<const uint4 *>(p.xg + ((size_t)t * p.xblocks * 4 + kg) * kGRec);
-  } else {
-    const uint32_t pr = col_ok ? pair : 0;
-    vrec = reinterpret_cast<const uint4 *>(p.hg + ((size_t)pr * p.hblocks * 4 + kg) * kGRec);
+  // the lane's record of block 0 (block b's is 4 records = 8 uint4 further):
+  // one 32 x 32 -> 64-bit multiply of the vector index by the record stride
+  const uint4 *vrec;
+  {
+    const uint32_t v = col_ok ? (FUSED ? pair / p.top_k : pair) : 0u;
+    const uint32_t stride = (FUSED ? p.xblocks : p.hblocks) * 8u;
+    vrec = reinterpret_cast<const uint4 *>(FUSED ? p.xg : p.hg) + ((uint64_t)v * stride + kg * 2u);
   }
 
-  float acc[4][4];
+  float acc[RT][4];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < RT; ++a)
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[a][i] = 0.f;
 
   // B operands of this wave's blocks of stage s (wave, wave + 4, ...) live
   // in slot s & 1.  A lane without a valid block (or a stage past the last)
   // reads block 0 of its record and gets a zero scale.
-  uint2 bv[2][kGWaveBlocks][3];
-  float bs[2][kGWaveBlocks];
-  bool bok[2][kGWaveBlocks];
+  uint2 bv[2][kWB][3];
+  float bs[2][kWB];
+  bool bok[2][kWB];
   auto load_b = [&](uint32_t s, int slot) {
-    const uint32_t left = s < n_stages ? kblocks - s * kGStageBlocks : 0u;
+    const uint32_t left = s < n_stages ? kblocks - s * kSB : 0u;
 #pragma unroll
-    for (int j = 0; j < kGWaveBlocks; ++j) {
+    for (int j = 0; j < kWB; ++j) {
       const uint32_t b = wave + 4 * j;
       bok[slot][j] = col_ok && b < left;
-      const uint32_t gb = bok[slot][j] ? s * kGStageBlocks + b : 0u;
+      const uint32_t gb = bok[slot][j] ? s * kSB + b : 0u;
       const uint4 *rp = vrec + gb * 8u;
       const uint4 r0 = rp[0], r1 = rp[1];
       bv[slot][j][0] = make_uint2(r0.x, r0.y);
@@ -408,17 +416,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerE
   // B(s + 1), W(s + 2)), so the wait counts are the same on the first round
   // as on every later one.  (Measured, config 3 gate/up: one slab with two
   // barriers per stage 69 us, two slabs 61-63 us.)
-  sg.load(0, row_chunks, wbuf[0]);
   load_b(0, 0);
-  sg.load(1, row_chunks, wbuf[1]);
+  __builtin_amdgcn_sched_barrier(0);  // B(0) issued before the wait for W(0)
   sg.store(wbuf[0], lq_buf[0], ld_buf[0]);
   __syncthreads();
   auto stage = [&](uint32_t s, int slot) {
     const uint8_t *sl = lq_buf[slot];
     const float *sd = ld_buf[slot];
-    const uint32_t nb = min(kGStageBlocks, kblocks - s * kGStageBlocks);
+    const uint32_t nb = min(kSB, kblocks - s * kSB);
 #pragma unroll
-    for (int j = 0; j < kGWaveBlocks; ++j) {
+    for (int j = 0; j < kWB; ++j) {
       const uint32_t b = wave + 4 * j;
       if (b >= nb) break;  // uniform
       const float bsj = bok[slot][j] ? bs[slot][j] : 0.f;
@@ -426,13 +433,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerE
 #pragma unroll
       for (int k = 0; k < 3; ++k) bk[k] = (long)(((uint64_t)bv[slot][j][k].y << 32) | bv[slot][j][k].x);
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const long av = *reinterpret_cast<const long *>(sl + (a * 16 + col) * kGRowStride + b * 32 + kg * 8);
+      for (int a = 0; a < RT; ++a) {
+        const long av = *reinterpret_cast<const long *>(sl + (a * 16 + col) * kStride + b * 32 + kg * 8);
         const v4i z = {0, 0, 0, 0};
         const v4i p0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[0], z, 0, 0, 0);
         const v4i p1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[1], z, 0, 0, 0);
         const v4i p2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bk[2], z, 0, 0, 0);
-        const float4 d = *reinterpret_cast<const float4 *>(&sd[b * kGScaleStride + a * 16 + kg * 4]);
+        const float4 d = *reinterpret_cast<const float4 *>(&sd[b * kSS + a * 16 + kg * 4]);
         const float dd[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -455,55 +462,68 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerE
     }
   }
 
-  // sum the four waves' partials (in the slab's LDS, free now); wave w
-  // then owns row tile w
-  typedef float RedT[4][64][4];  // [row tile][lane][i]
+  // Sum the four waves' partials (in the slabs' LDS, free now): wave w
+  // then owns row tiles w, w + 4, ...
+  constexpr int kOwn = RT / 4;
+  typedef float RedT[RT][64][4];  // [row tile][lane][i]
   RedT *red = reinterpret_cast<RedT *>(lq);
+  static_assert(sizeof(RedT) * 4 <= sizeof(lq_buf), "reduction fits in the slabs");
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < RT; ++a)
     *reinterpret_cast<float4 *>(&red[wave][a][lane][0]) = make_float4(acc[a][0], acc[a][1], acc[a][2], acc[a][3]);
   __syncthreads();
-  float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 sum[kOwn];
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {  // fixed order
-    const float4 v = *reinterpret_cast<const float4 *>(&red[w][wave][lane][0]);
-    sum.x += v.x;
-    sum.y += v.y;
-    sum.z += v.z;
-    sum.w += v.w;
+  for (int o = 0; o < kOwn; ++o) {
+    sum[o] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {  // fixed order
+      const float4 v = *reinterpret_cast<const float4 *>(&red[w][wave + 4 * o][lane][0]);
+      sum[o].x += v.x;
+      sum[o].y += v.y;
+      sum[o].z += v.z;
+      sum[o].w += v.w;
+    }
   }
-  // lane holds rows wave*16 + 4*kg + i of column col
+  // lane holds rows (wave + 4 o) * 16 + 4 * kg + i of column col
 
   if constexpr (FUSED) {
     __syncthreads();
-    float *fin = reinterpret_cast<float *>(lq);  // [64 rows][16 cols]
-    const uint32_t r = wave * 16 + 4 * kg;
-    fin[(r + 0) * kGTok + col] = sum.x;
-    fin[(r + 1) * kGTok + col] = sum.y;
-    fin[(r + 2) * kGTok + col] = sum.z;
-    fin[(r + 3) * kGTok + col] = sum.w;
+    float *fin = reinterpret_cast<float *>(lq);  // [16 RT rows][16 cols]
+#pragma unroll
+    for (int o = 0; o < kOwn; ++o) {
+      const uint32_t r = (wave + 4 * o) * 16 + 4 * kg;
+      fin[(r + 0) * kGTok + col] = sum[o].x;
+      fin[(r + 1) * kGTok + col] = sum[o].y;
+      fin[(r + 2) * kGTok + col] = sum[o].z;
+      fin[(r + 3) * kGTok + col] = sum[o].w;
+    }
     __syncthreads();
-    if (tid < 64) {
-      // pair column c = tid / 4, k-group m = tid % 4: h rows 8m .. 8m+7
-      const uint32_t c = tid / 4, m = tid % 4;
+    if (tid < 64 * kOwn) {
+      // h block hk of the workgroup, pair column c, k-group m: h rows
+      // 32 hk + 8m .. +7 (gate rows there, up rows 8 RT further)
+      const uint32_t hk = tid / 64, c = (tid / 4) % 16, m = tid % 4;
       float h[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float g = fin[(8 * m + i) * kGTok + c];
-        const float u = fin[(32 + 8 * m + i) * kGTok + c];
+        const float g = fin[(32 * hk + 8 * m + i) * kGTok + c];
+        const float u = fin[(kRows / 2 + 32 * hk + 8 * m + i) * kGTok + c];
         h[i] = silu_mul(g, u, p.swiglu_limit);
       }
-      const uint32_t pr = s_pair[c];
+      const uint32_t pr = __shfl(pair, (int)c, 64);  // lane c of every wave holds column c's pair
       const bool ok = pr != 0xffffffffu;
-      const size_t hb = (size_t)(ok ? pr : 0) * p.hblocks + rt;
+      const size_t hb = (size_t)(ok ? pr : 0) * p.hblocks + rt * kOwn + hk;
       quant_group(h, p.hg + (hb * 4 + m) * kGRec, ok);
     }
   } else {
     if (col_ok) {
       const float w = p.weights ? p.weights[pair] : 1.0f;
-      const uint32_t r = rt * kGRows + wave * 16 + 4 * kg;
-      *reinterpret_cast<float4 *>(p.partial + (size_t)pair * p.d_model + r) =
-          make_float4(w * sum.x, w * sum.y, w * sum.z, w * sum.w);
+#pragma unroll
+      for (int o = 0; o < kOwn; ++o) {
+        const uint32_t r = rt * kRows + (wave + 4 * o) * 16 + 4 * kg;
+        *reinterpret_cast<float4 *>(p.partial + (size_t)pair * p.d_model + r) =
+            make_float4(w * sum[o].x, w * sum[o].y, w * sum[o].z, w * sum[o].w);
+      }
     }
   }
 }
@@ -561,14 +581,25 @@ hipError_t launch_grouped_prep(const GroupedParams &p, hipStream_t st) {
 }
 
 hipError_t launch_grouped_proj(int fmt, bool fused, const GroupedParams &p, uint32_t max_tiles, hipStream_t st) {
-  const uint32_t grid = max_tiles * (fused ? p.d_ff / 32 : p.d_model / kGRows);
+  // Down runs 128-row workgroups (RT = 8) wherever d_model divides by 128;
+  // gate/up keeps 64-row workgroups (RT = 4).  Measured on config 3 (64
+  // tokens): down 38.9 -> 36.1 us with RT = 8 (256 tokens: 94 -> 75 us), but
+  // gate/up 62 -> 70 us, its launch then filling under one round of the
+  // resident workgroup slots.
+  const bool wide = !fused && p.d_model % 128 == 0;
+  const uint32_t rows = wide ? 128 : 64;
+  const uint32_t grid = max_tiles * (fused ? p.d_ff / (rows / 2) : p.d_model / rows);
+#define MER_GPROJ(F, FU, R) hipLaunchKernelGGL((gproj_kernel<F, FU, R>), dim3(grid), dim3(256), 0, st, p)
   if (fmt == FMT_Q4_0) {
-    if (fused) hipLaunchKernelGGL((gproj_kernel<FMT_Q4_0, true>), dim3(grid), dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((gproj_kernel<FMT_Q4_0, false>), dim3(grid), dim3(256), 0, st, p);
+    if (fused) MER_GPROJ(FMT_Q4_0, true, 4);
+    else if (wide) MER_GPROJ(FMT_Q4_0, false, 8);
+    else MER_GPROJ(FMT_Q4_0, false, 4);
   } else {
-    if (fused) hipLaunchKernelGGL((gproj_kernel<FMT_Q8_0, true>), dim3(grid), dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((gproj_kernel<FMT_Q8_0, false>), dim3(grid), dim3(256), 0, st, p);
+    if (fused) MER_GPROJ(FMT_Q8_0, true, 4);
+    else if (wide) MER_GPROJ(FMT_Q8_0, false, 8);
+    else MER_GPROJ(FMT_Q8_0, false, 4);
   }
+#undef MER_GPROJ
   return hipGetLastError();
 }
 
