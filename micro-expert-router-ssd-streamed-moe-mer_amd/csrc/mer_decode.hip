@@ -310,6 +310,7 @@ template <int FMT, int G, int R, int S, int NB>
 struct TileWalk {
   using T = FmtTraits<FMT>;
   static constexpr int kGroups = 64 / G;
+  static constexpr int kRows = R;  // rows of a lane group per pass
   static constexpr uint32_t kStep = R * kGroups;
   static constexpr uint32_t kPasses = kTileRows / kStep;
   static_assert(kTileRows % kStep == 0 && kPasses % NB == 0, "passes must tile 32 rows in whole buffer rounds");
@@ -550,7 +551,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       const bool valid = expert && gl < p.g_cps && c < p.g_chunks;
       const uint8_t *const bases[2] = {expert, expert + p.proj_bytes};
       W walk;
-      walk.init(bases, p.g_chunks * (uint32_t)FmtTraits<FMT>::kChunkBytes, c, valid, tile * kTileRows + grp * 2);
+      walk.init(bases, p.g_chunks * (uint32_t)FmtTraits<FMT>::kChunkBytes, c, valid, tile * kTileRows + grp * W::kRows);
       typename W::WBuf wbuf[kBuffers];
       walk.prefetch(wbuf);
       wait_input(t);
@@ -622,7 +623,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       const uint8_t *const bases[1] = {expert + 2 * p.proj_bytes};
       W walk;
       walk.init(bases, p.d_chunks * (uint32_t)FmtTraits<FMT>::kChunkBytes, c, valid,
-                tile * kTileRows + grp * (GD == 16 ? 2 : 4));
+                tile * kTileRows + grp * W::kRows);
       typename W::WBuf wbuf[kBuffers];
       walk.prefetch(wbuf);
       // the h planes of this column slice
