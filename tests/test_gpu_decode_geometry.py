@@ -1,0 +1,71 @@
+"""Every instantiation of the persistent decode kernel against the oracle.
+
+The decode kernel is compiled per (weight format, gate/up lane-group width
+GG, down lane-group width GD), 2 x 3 x 3 = 18 variants; the planner picks
+one from the shape (column chunks per slice <= 16, <= 32 or <= 64 lanes),
+the number of routed instances (narrow layers split gate/up rows into two
+column slices) and the down rows' length (32-chunk slices when they
+divide).  Each case below is built to land on one variant; `_plan` mirrors
+the planner's rule so a change of the rule shows up here as a failed
+geometry assertion rather than as silently lost coverage.  Bar:
+assert_ffn_close against the oracle's routed forward and slot-order combine."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from test_gpu_parity import Q4, Q8, _oracle_moe, _table, assert_ffn_close, make_expert, say, to_dev  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+def _group_width(chunks: int, min_slices: int = 1) -> int:
+    slices = max(-(-chunks // 64), min_slices)
+    cps = -(-chunks // slices)
+    return 16 if cps <= 16 else (32 if cps <= 32 else 64)
+
+
+def _plan(dm: int, dff: int, n_tok: int, k: int) -> tuple[int, int]:
+    """(GG, GD) as plan_decode chooses them (mer_abi.hip)."""
+    g_chunks, d_chunks = dm // 64, dff // 64
+    narrow = n_tok * k * (dff // 32) < 512 and g_chunks >= 32
+    d32 = d_chunks > 64 and d_chunks % 32 == 0 and k * (d_chunks // 32) <= 16
+    return _group_width(g_chunks, 2 if narrow else 1), _group_width(d_chunks, d_chunks // 32 if d32 else 1)
+
+
+# (d_model, d_ff, tokens, top_k) -> (GG, GD)
+SHAPES = {
+    (1024, 1024, 2, 2): (16, 16),
+    (1024, 2048, 2, 2): (16, 32),
+    (1024, 4096, 1, 2): (16, 64),
+    (2048, 1024, 8, 2): (32, 16),
+    (2048, 2048, 4, 2): (32, 32),
+    (4096, 4096, 1, 2): (32, 64),   # narrow: two 32-chunk gate/up slices
+    (4096, 1024, 8, 2): (64, 16),
+    (4096, 2048, 4, 2): (64, 32),
+    (4096, 4096, 2, 2): (64, 64),
+}
+CASES = [(dt, *shape) for dt in (Q4, Q8) for shape in SHAPES]
+
+
+@pytest.mark.parametrize("dtype,dm,dff,n_tok,k", CASES)
+def test_decode_variant_vs_oracle(mer, oracle, gpu, dtype, dm, dff, n_tok, k):
+    gg, gd = SHAPES[(dm, dff, n_tok, k)]
+    assert _plan(dm, dff, n_tok, k) == (gg, gd)
+    say(f"decode variant fmt={dtype} GG={gg} GD={gd}: dm={dm} dff={dff} tokens={n_tok} top_k={k}")
+    rng = np.random.default_rng(dm * 7 + dff + 13 * n_tok + dtype)
+    n_exp = 3
+    blobs = [make_expert(oracle, dtype, dm, dff, 700 + e) for e in range(n_exp)]
+    devs, table = _table(blobs, gpu)
+    ids = np.stack([rng.choice(n_exp, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    w = rng.random((n_tok, k)).astype(np.float32)
+    x = rng.standard_normal((n_tok, dm)).astype(np.float32)
+    want = _oracle_moe(oracle, dtype, blobs, ids, w, x, dm, dff)
+    got = mer.moe_forward(mer.WeightDtype(dtype), dm, dff, table, to_dev(ids, gpu), to_dev(w, gpu),
+                          to_dev(x, gpu)).cpu().numpy()
+    torch.cuda.synchronize()
+    mer.take_device_status()
+    assert_ffn_close(got, want, f"decode variant fmt={dtype} GG={gg} GD={gd}")
+    del devs
