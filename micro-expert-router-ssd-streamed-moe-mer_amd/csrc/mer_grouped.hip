@@ -158,7 +158,9 @@ __global__ __launch_bounds__(1024) void group_kernel(GroupedParams p) {
   extern __shared__ uint32_t sh[];
   uint32_t *cnt = sh;                   // [table_len] pairs per expert, then offsets
   uint32_t *tcnt = sh + p.table_len;    // [table_len] tiles per expert, then offsets
-  uint32_t *pos = tcnt + p.table_len;   // [n_pairs] rank of a pair within its expert
+  // [n_pairs] the pair's expert << 16 | its rank within the expert (both
+  // < 4096), so the final scatter needs no second read of the routing
+  uint32_t *pos = tcnt + p.table_len;
   __shared__ uint32_t part[1024 * 2];
   const uint32_t tid = threadIdx.x, nth = blockDim.x;
   for (uint32_t e = tid; e < p.table_len; e += nth) cnt[e] = 0u;
@@ -168,7 +170,8 @@ __global__ __launch_bounds__(1024) void group_kernel(GroupedParams p) {
     const bool ok = pair_valid(p, q, &blob);
     p.pair_ok[q] = ok ? 1u : 0u;
     if (ok) {
-      pos[q] = atomicAdd(&cnt[p.ids[q]], 1u);
+      const uint32_t e = (uint32_t)p.ids[q];
+      pos[q] = (e << 16) | atomicAdd(&cnt[e], 1u);
     } else {
       pos[q] = 0xffffffffu;
       if (!(p.weights && p.weights[q] == 0.0f)) record_status(p.status, 16u /* MER_ERR_RESIDENCY_MISS */);
@@ -230,7 +233,7 @@ __global__ __launch_bounds__(1024) void group_kernel(GroupedParams p) {
   if (tid == nth - 1) *p.n_tiles = it;
   __syncthreads();
   for (uint32_t q = tid; q < p.n_pairs; q += nth)
-    if (pos[q] != 0xffffffffu) p.plist[cnt[p.ids[q]] + pos[q]] = q;
+    if (pos[q] != 0xffffffffu) p.plist[cnt[pos[q] >> 16] + (pos[q] & 0xffffu)] = q;
 }
 
 // Stage one (16 RT)-row x (32 / RT)-block slab of weights into LDS: one
