@@ -96,6 +96,31 @@ def test_grouped_qwen3_batch_config(mer, oracle, gpu):
     del devs
 
 
+@pytest.mark.parametrize("name,dm,dff,n_exp,n_tok,k", [
+    ("mixtral", 4096, 14336, 8, 12, 2),    # Mixtral-shape Q4_0 prefill chunk
+    ("deepseek", 7168, 2048, 16, 16, 8),   # DeepSeek-V3 routed-expert shape
+])
+def test_grouped_q4_model_shapes(mer, oracle, gpu, name, dm, dff, n_exp, n_tok, k):
+    """The grouped path at the Q4_0 model shapes of the decode configs, with
+    residual: K of 4096 and 7168 (16 and 28 gate/up stages, 56 and 16 down
+    stages), more pairs per expert than one 16-pair tile for the popular
+    ones, and the decode path on the same batch as a second opinion."""
+    say(f"grouped {name} Q4_0 {n_tok} tokens x {n_exp} experts top-{k}")
+    blobs = [make_expert(oracle, Q4, dm, dff, 40 + e) for e in range(n_exp)]
+    devs, table = _table(blobs, gpu)
+    ids, w = routing.zipf_skewed_routes(n_tok, n_exp, k, 1.0, seed=11)
+    x = np.random.default_rng(21).standard_normal((n_tok, dm)).astype(np.float32)
+    want = oracle_moe(oracle, Q4, blobs, ids, w, x, dm, dff) + x
+    got = mer.moe_grouped(mer.WeightDtype.Q4_0, dm, dff, table, to_dev(ids, gpu), to_dev(w, gpu),
+                          to_dev(x, gpu), residual=True).cpu().numpy()
+    assert_ffn_close(got, want, f"grouped {name}")
+    dec = mer.moe_forward(mer.WeightDtype.Q4_0, dm, dff, table, to_dev(ids, gpu), to_dev(w, gpu),
+                          to_dev(x, gpu), residual=True).cpu().numpy()
+    assert_ffn_close(got, dec, f"grouped vs decode {name}")
+    mer.take_device_status()
+    del devs
+
+
 def test_grouped_missing_expert_records_residency_miss(mer, oracle, gpu):
     dm, dff = 128, 128
     say("grouped missing expert")
