@@ -224,27 +224,46 @@ __device__ __forceinline__ void trace_item(const DecodeParams &p, uint64_t gi, c
   r[7] = m.extra;
 }
 
-// Sum of v over each group of G adjacent lanes (G = 16, 32 or 64), on every
-// lane of the group.  Row sums (16 lanes) take four DPP row rotations,
-// which cost a VALU op each; rows are then combined through readlane
-// (uniform values) instead of LDS-routed lane permutes.
-template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128 /* row_ror:8 */, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124 /* row_ror:4 */, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x122 /* row_ror:2 */, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x121 /* row_ror:1 */, 0xf, 0xf, false));
-  if constexpr (G == 16) {
-    return v;
+// One step of the transposed row reduction at lane distance D: lanes whose
+// bit D is clear keep a, the others keep b, and each adds its partner's
+// copy (lane l^D for D >= 8, the mirror lane 7-l of an 8-lane half for
+// D = 4), so the result holds a partial sum of a on the lower lanes of each
+// 2D block and of b on the upper ones, each spread over D lanes.  D = 32
+// and 16 use the lane swaps across 32- and 16-lane halves, D <= 8 DPP.
+template <int D>
+__device__ __forceinline__ float split_sum(float a, float b) {
+  if constexpr (D == 32 || D == 16) {
+    const auto r = D == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false)
+                           : __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
   } else {
-    const int b = __float_as_int(v);
-    const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
-    const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
-    const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
-    const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
-    if constexpr (G == 32) return (threadIdx.x & 32u) ? r2 + r3 : r0 + r1;
-    else return (r0 + r1) + (r2 + r3);
+    static_assert(D == 8 || D == 4, "split distance");
+    constexpr int kCtrl = D == 8 ? 0x128 /* row_ror:8 */ : 0x141 /* row_half_mirror */;
+    const bool hi = threadIdx.x & D;
+    const float keep = hi ? b : a, send = hi ? a : b;
+    return keep + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), kCtrl, 0xf, 0xf, true));
   }
+}
+
+// Sum over each aligned block of N lanes (N = 4, 8 or 16), on every lane of
+// the block, by DPP adds.  Every pattern used reads a lane inside the same
+// row, so bound_ctrl (zero for a source outside the row) never applies; it
+// is set because it lets the compiler fold each move into its add.
+template <int N>
+__device__ __forceinline__ float span_sum(float v) {
+  static_assert(N == 4 || N == 8 || N == 16, "span");
+  auto add = [](float x, auto ctrl) {
+    return x + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, true));
+  };
+  if constexpr (N == 16) {
+    v = add(v, std::integral_constant<int, 0x128>{});  // row_ror:8
+    v = add(v, std::integral_constant<int, 0x124>{});  // row_ror:4
+  } else if constexpr (N == 8) {
+    v = add(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
+  }
+  v = add(v, std::integral_constant<int, 0x4e>{});  // quad_perm [2,3,0,1]
+  v = add(v, std::integral_constant<int, 0xb1>{});  // quad_perm [1,0,3,2]
+  return v;
 }
 
 // Quantise `nblocks` (<= 64 / groups) blocks of x into digit planes in line
@@ -302,8 +321,14 @@ __device__ __forceinline__ void pack_blocks(const float *x, uint32_t nblocks, ui
 // pass, S weight streams (2 = gate and up).  Weight loads are raw buffer
 // loads: a lane without a chunk gets an offset past the buffer's range and
 // reads zeros, so the load sequence is branch-free and the compiler can
-// keep exactly the next passes' loads outstanding.  `emit(row, acc[S])`
-// receives each row's sums on all lanes of the owning group.
+// keep exactly the next passes' loads outstanding.  The V = S*R sums of a
+// pass are reduced transposed: split steps at lane distances G/2, G/4, ...
+// halve the values per lane and the lanes per value together, so that
+// after log2(V) steps each lane holds one value spread over G/V lanes, and
+// DPP adds finish it (10 VALU ops for V = 4 on 64 or 32 lanes, against 44
+// for four separate group sums).  `emit(writer, row, s, sum)` then runs on
+// every lane with the lane's row and stream; one lane per value is the
+// writer.
 constexpr uint32_t kNoChunk = 0x80000000u;  // beyond num_records: loads return 0
 
 template <int FMT, int G, int R, int S, int NB>
@@ -314,12 +339,18 @@ struct TileWalk {
   static constexpr uint32_t kStep = R * kGroups;
   static constexpr uint32_t kPasses = kTileRows / kStep;
   static_assert(kTileRows % kStep == 0 && kPasses % NB == 0, "passes must tile 32 rows in whole buffer rounds");
+  static constexpr int kV = S * R;       // sums per lane and pass
+  static constexpr int kSpan = G / kV;   // lanes over which one reduced sum lies
+  static_assert((kV & (kV - 1)) == 0 && kSpan >= 4 && kSpan <= 16, "reduction shape");
   using WBuf = uint32_t[S][R][T::kChunkDwords];
 
   __amdgpu_buffer_rsrc_t rsrc[S];
   uint32_t row_bytes;
   uint32_t voff;    // byte offset of the lane's chunk in row r_base (kNoChunk if none)
   uint32_t r_base;  // first row of this lane group's first pass
+  uint32_t my_row;  // r_base + the row of the sum this lane ends with
+  int my_s;         // stream of that sum
+  bool writer;      // first lane of its sum's span
 
   __device__ __forceinline__ void init(const uint8_t *const (&base)[S], uint32_t row_bytes_, uint32_t chunk,
                                        bool valid, uint32_t r_base_) {
@@ -329,6 +360,29 @@ struct TileWalk {
     row_bytes = row_bytes_;
     r_base = r_base_;
     voff = valid ? r_base_ * row_bytes_ + chunk * (uint32_t)T::kChunkBytes : kNoChunk;
+    // value index k = s*R + j: the lane's bits at the split distances,
+    // most significant first
+    const uint32_t k = (threadIdx.x % G) / kSpan;
+    my_row = r_base_ + k % R;
+    my_s = (int)(k / R);
+    writer = threadIdx.x % kSpan == 0;
+  }
+
+  __device__ __forceinline__ float reduce(float (&v)[kV]) const {
+    if constexpr (kV >= 2) {
+#pragma unroll
+      for (int i = 0; i < kV / 2; ++i) v[i] = split_sum<G / 2>(v[i], v[i + kV / 2]);
+    }
+    if constexpr (kV >= 4) {
+#pragma unroll
+      for (int i = 0; i < kV / 4; ++i) v[i] = split_sum<G / 4>(v[i], v[i + kV / 4]);
+    }
+    if constexpr (kV >= 8) {
+#pragma unroll
+      for (int i = 0; i < kV / 8; ++i) v[i] = split_sum<G / 8>(v[i], v[i + kV / 8]);
+    }
+    static_assert(kV <= 8, "at most three split steps");
+    return span_sum<kSpan>(v[0]);
   }
 
   __device__ __forceinline__ void load(uint32_t pass, WBuf &wb) const {
@@ -353,18 +407,12 @@ struct TileWalk {
   template <class Emit>
   __device__ __forceinline__ void compute(uint32_t pass, WBuf &wb, const uint32_t *xd, const float *xsc,
                                           Emit &&emit) const {
-    float acc[S][R];
+    float v[kV];
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
-      for (int j = 0; j < R; ++j) acc[s][j] = group_sum<G>(chunk_idot<FMT>(wb[s][j], xd, xsc));
-#pragma unroll
-    for (int j = 0; j < R; ++j) {
-      float a[S];
-#pragma unroll
-      for (int s = 0; s < S; ++s) a[s] = acc[s][j];
-      emit(r_base + pass * kStep + j, a);
-    }
+      for (int j = 0; j < R; ++j) v[s * R + j] = chunk_idot<FMT>(wb[s][j], xd, xsc);
+    emit(writer, my_row + pass * kStep, my_s, reduce(v));
   }
 
   // Issue the loads of passes 0 .. NB-1 into the NB buffers.
@@ -448,8 +496,9 @@ __device__ __forceinline__ void fetch_digits(const uint32_t *dig, size_t block0,
 }  // namespace
 
 template <int FMT, int GG, int GD>
-__global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q4_0 ? 3 : 2))) void decode_kernel(DecodeParams p) {
   __shared__ float s_h[kTileRows];
+  __shared__ float s_gu[2 * kTileRows];  // gate and up row sums of a single-slice G item
   const uint32_t lane = lane_id();
   using D = DigitTraits<FMT>;
   constexpr uint32_t kPackBlocks = 64 / D::kGroups;
@@ -564,21 +613,20 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       tm.fetched = trace_now(p);
       float *gpart = p.gpart + (((size_t)l * p.n_inst + inst) * p.g_slices + gs) * 2 * p.d_ff;
       const bool single_slice = p.g_slices == 1;
-      auto emit = [&](uint32_t r, const float (&a)[2]) {
-        if (gl == 0) {
-          if (single_slice) {
-            s_h[r - tile * kTileRows] = expert ? silu_mul(a[0], a[1], p.swiglu_limit) : 0.f;
-          } else {
-            st_dev(gpart + r, a[0]);
-            st_dev(gpart + p.d_ff + r, a[1]);
-          }
+      auto emit = [&](bool writer, uint32_t r, int s, float a) {
+        if (writer) {
+          if (single_slice) s_gu[s * kTileRows + r - tile * kTileRows] = a;
+          else st_dev(gpart + (size_t)s * p.d_ff + r, a);
         }
       };
       walk.run(wbuf, xd, xsc, emit);
       prio_hi();
       tm.walked = trace_now(p);
       bool pack = single_slice;
-      if (!single_slice) {
+      if (single_slice) {
+        __syncthreads();
+        if (lane < kTileRows) s_h[lane] = expert ? silu_mul(s_gu[lane], s_gu[kTileRows + lane], p.swiglu_limit) : 0.f;
+      } else {
         pack = arrive_last(cnt + p.c_ga + (size_t)inst * p.g_tiles + tile, p.g_slices);
         if (pack && lane < kTileRows) {
           const size_t base = ((size_t)l * p.n_inst + inst) * p.g_slices * 2 * p.d_ff;
@@ -643,8 +691,8 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeParams p) {
       // is applied here; a zero-weight slot contributes exactly nothing, as
       // the engine skips it (engine.rs:5575-5580).
       const float w_slot = la.weights ? la.weights[t * p.top_k + slot] : 1.0f;
-      auto emit = [&](uint32_t r, const float (&a)[1]) {
-        if (gl == 0) s_h[r - tile * kTileRows] = a[0];
+      auto emit = [&](bool writer, uint32_t r, int, float a) {
+        if (writer) s_h[r - tile * kTileRows] = a;
       };
       walk.run(wbuf, xd, xsc, emit);
       prio_hi();
