@@ -584,21 +584,25 @@ hipError_t launch_grouped_prep(const GroupedParams &p, hipStream_t st) {
 }
 
 hipError_t launch_grouped_proj(int fmt, bool fused, const GroupedParams &p, uint32_t max_tiles, hipStream_t st) {
-  // Down runs 128-row workgroups (RT = 8) wherever d_model divides by 128;
-  // gate/up keeps 64-row workgroups (RT = 4).  Measured on config 3 (64
-  // tokens): down 38.9 -> 36.1 us with RT = 8 (256 tokens: 94 -> 75 us), but
-  // gate/up 62 -> 70 us, its launch then filling under one round of the
-  // resident workgroup slots.
-  const bool wide = !fused && p.d_model % 128 == 0;
+  // Down runs 128-row workgroups (RT = 8) wherever d_model divides by 128.
+  // Gate/up does so (64 gate + 64 up rows) only from 2048 routed pairs on:
+  // with fewer its launch fills too few rounds of the resident workgroup
+  // slots.  Measured on the Qwen3 Q8_0 shape, gate/up us at RT = 4 / 8:
+  // 16 tokens 36.7 / 41.1, 64 tokens 62.2 / 69.2, 128 tokens 89.2 / 92.1,
+  // 256 tokens 144.6 / 136.4; down at 64 tokens 38.9 -> 36.1, at 256
+  // tokens 94 -> 75.
+  const bool wide = fused ? (p.d_ff % 64 == 0 && p.n_pairs >= 2048) : p.d_model % 128 == 0;
   const uint32_t rows = wide ? 128 : 64;
   const uint32_t grid = max_tiles * (fused ? p.d_ff / (rows / 2) : p.d_model / rows);
 #define MER_GPROJ(F, FU, R) hipLaunchKernelGGL((gproj_kernel<F, FU, R>), dim3(grid), dim3(256), 0, st, p)
   if (fmt == FMT_Q4_0) {
-    if (fused) MER_GPROJ(FMT_Q4_0, true, 4);
+    if (fused && wide) MER_GPROJ(FMT_Q4_0, true, 8);
+    else if (fused) MER_GPROJ(FMT_Q4_0, true, 4);
     else if (wide) MER_GPROJ(FMT_Q4_0, false, 8);
     else MER_GPROJ(FMT_Q4_0, false, 4);
   } else {
-    if (fused) MER_GPROJ(FMT_Q8_0, true, 4);
+    if (fused && wide) MER_GPROJ(FMT_Q8_0, true, 8);
+    else if (fused) MER_GPROJ(FMT_Q8_0, true, 4);
     else if (wide) MER_GPROJ(FMT_Q8_0, false, 8);
     else MER_GPROJ(FMT_Q8_0, false, 4);
   }

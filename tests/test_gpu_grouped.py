@@ -48,6 +48,8 @@ def oracle_moe(oracle, dtype, blobs, ids, w, x, dm, dff, table_ok=None):
     (Q4, 512, 1024, 16, 24, 4),   # gate/up K over two LDS stages
     (Q8, 192, 128, 5, 20, 2),     # d_model % 128 != 0: 64-row down workgroups
     (Q4, 320, 64, 4, 9, 3),       # the same for Q4_0, one h block per pair
+    (Q4, 128, 128, 16, 256, 8),   # 2048 pairs: 128-row gate/up workgroups
+    (Q8, 256, 192, 12, 300, 7),   # 2100 pairs, the same for Q8_0
 ])
 def test_grouped_vs_oracle(mer, oracle, gpu, dtype, dm, dff, n_exp, n_tok, k):
     say(f"grouped dtype={dtype} dm={dm} dff={dff} experts={n_exp} tokens={n_tok} k={k}")
