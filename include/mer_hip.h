@@ -26,17 +26,32 @@
  *     parallel expert workers, or several concurrent dispatches, each
  *     with its own stream: backend/mod.rs:1346-1432, :2685-2697).  Calls
  *     on one stream from several threads are serialised by the stream's
- *     workspace lock and run in stream order.  The persistent decode
- *     kernel claims its work items in order from a counter, so it
- *     completes whatever else runs on the device (it needs no
- *     co-residency of its grid).  Release a stream's workspace with
- *     mer_hip_stream_release before destroying the stream.
+ *     workspace lock and run in stream order.  Release a stream's
+ *     workspace with mer_hip_stream_release before destroying the stream;
+ *     a release must not overlap calls on that stream (such a call fails
+ *     with MER_ERR_RUNTIME_INVARIANT).
+ *   - The persistent decode kernel (mer_hip_moe_forward[_noalloc],
+ *     mer_hip_moe_forward_layers, mer_hip_expert_forward for decode shapes)
+ *     hands its work items to its workgroups by static stride, so it needs
+ *     its whole grid resident to finish.  The library therefore orders all
+ *     decode launches of a device one after another on the GPU, whatever
+ *     their streams: a launch on another stream than the previous one
+ *     waits (hipStreamWaitEvent, no host blocking) for that launch to end.
+ *     Two decode grids are never in flight together; other kernels beside
+ *     one only delay it.  The library makes no progress guarantee when a
+ *     caller runs its own persistent or spin-waiting kernels on the device
+ *     at the same time: a decode wait gives up after 2 s with
+ *     MER_ERR_RUNTIME_INVARIANT (never a hang).
  *   - Graph capture: every device entry point may be captured into a HIP
  *     graph once a call of the same shape has run on that stream (the
  *     workspace grows only outside capture; growth under capture fails
  *     with MER_ERR_PHYSICAL_CAPACITY).  Replays are correct: the decode
  *     kernel's epoch lives in device memory and each launch hands the
- *     next one a fresh value.
+ *     next one a fresh value.  A captured graph holds the workspace's
+ *     buffer addresses: a later call of a larger shape on that stream
+ *     (which grows the workspace) or mer_hip_stream_release invalidates
+ *     graphs captured on it.  Captured decode launches are not ordered
+ *     against decode calls on other streams; the caller orders replays.
  */
 #ifndef MER_HIP_H
 #define MER_HIP_H
@@ -233,9 +248,11 @@ int mer_hip_moe_forward(int dtype, size_t d_model, size_t d_ff,
  * Mixtral-shape top-2 token needs 0.41 MiB, so up to 19 such tokens fit).  The call allocates
  * nothing and enqueues two kernels (scratch preparation, decode).  Every
  * call on a GPU shares that GPU's array, which keeps the last call's
- * contents: calls that overlap on one GPU (two streams, or two threads
- * without ordering) race and give wrong results; order them on one
- * stream. */
+ * contents.  Calls from any streams and threads are ordered on the GPU
+ * like every decode launch (see the conventions above), so they never
+ * overlap; under graph capture that ordering is the caller's: replays of
+ * graphs holding no-alloc calls must not overlap other no-alloc calls on
+ * the same GPU. */
 int mer_hip_moe_forward_noalloc(int dtype, size_t d_model, size_t d_ff,
                                 size_t n_tokens, size_t top_k,
                                 const void *const *d_expert_table, size_t table_len,
@@ -304,8 +321,9 @@ typedef struct mer_layer_args {
  * output), with the same combine order and flags as mer_hip_moe_forward;
  * under MER_MOE_CHAIN layer l's input is layer l-1's out.  Requires
  * d_model and d_ff to be multiples of 64.  The launch sizes its grid to
- * fill every CU; other work on the device (other streams) shares the CUs
- * and slows it, but cannot stall it (items are claimed in order). */
+ * fill every CU; its workgroups take items by static stride, so it runs
+ * after any earlier decode launch of the device (see the conventions);
+ * ordinary kernels on other streams share the CUs and only slow it. */
 int mer_hip_moe_forward_layers(int dtype, size_t d_model, size_t d_ff, size_t n_layers, size_t n_tokens,
                                size_t top_k, const mer_layer_args *layers, unsigned flags, void *stream);
 

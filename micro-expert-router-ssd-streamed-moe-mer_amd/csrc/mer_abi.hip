@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <functional>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -74,6 +75,7 @@ int fmt_of(int dtype) { return dtype == MER_DTYPE_Q4_0 ? FMT_Q4_0 : FMT_Q8_0; }
 // host and ordered on the device by the stream.
 struct Workspace {
   std::mutex mu;
+  bool released = false;         // set (under mu) by mer_hip_stream_release / mer_hip_shutdown
   hipStream_t stream = nullptr;
   float *scratch = nullptr;      // h vectors, digit lines, partial sums
   size_t scratch_floats = 0;
@@ -97,18 +99,25 @@ struct DeviceState {
   uint32_t *status = nullptr;
   uint64_t clock_khz = 100000;
   std::atomic<int> occupancy[2][3][3] = {};  // resident decode workgroups per CU, by (fmt, GG, GD)
-  // The first stream to launch the persistent decode kernel on this device.
-  // Its launches are plain; every other stream's are cooperative.  Plain
-  // launches (one stream, so one at a time) wait, if other kernels hold CUs,
-  // only until those kernels finish; cooperative grids are resident whole.
-  // So no two partly resident persistent grids can ever wait on each other,
-  // and a single engine stream does not pay the cooperative launch's extra
-  // ~16 us per launch.
-  std::atomic<uintptr_t> primary_stream{UINTPTR_MAX};
+  // Device-wide order of persistent decode launches (guarded by
+  // g_launch_mu).  The decode grid fills the device and hands items out by
+  // static stride, so it needs all of its workgroups resident; two such
+  // grids in flight at once could each hold part of the device while
+  // waiting for the rest.  Every launch therefore waits (on the GPU) for the
+  // previous one, from whichever stream it came: `decode_done` is recorded
+  // after each launch on its stream, and a launch on another stream waits
+  // for it first.  Grids of one device never overlap, which also orders the
+  // calls that share the no-alloc scratch array.  All launches are plain.
+  hipEvent_t decode_done = nullptr;
+  hipStream_t decode_last = nullptr;
+  bool decode_any = false;
   // This device's copy of the no-alloc scratch array (below), from
   // hipGetSymbolAddress at mer_hip_init.
   uint8_t *noalloc_scratch = nullptr;
-  std::unordered_map<hipStream_t, std::unique_ptr<Workspace>> ws;  // guarded by g_mu
+  // Workspaces are shared: a call holds its stream's workspace for its whole
+  // host part, so a concurrent mer_hip_stream_release cannot free the object
+  // under it (the call then finds it marked released and fails cleanly).
+  std::unordered_map<hipStream_t, std::shared_ptr<Workspace>> ws;  // guarded by g_mu
 };
 // Lock order: g_mu, then a workspace's mutex.  Code holding a workspace's
 // mutex takes only the leaf locks (g_timing_mu, g_trace_mu, g_launch_mu),
@@ -182,16 +191,23 @@ int hip_fail(hipError_t e, int status, const char *what) {
 }
 
 // The workspace of `st` on the current device, created on first use.
-Workspace *workspace_for(hipStream_t st) {
+std::shared_ptr<Workspace> workspace_for(hipStream_t st) {
   std::lock_guard<std::mutex> lock(g_mu);
   const int dv = g_device.load();
   if (dv < 0) return nullptr;
   auto &slot = g_dev[dv].ws[st];
   if (!slot) {
-    slot.reset(new Workspace());
+    slot = std::make_shared<Workspace>();
     slot->stream = st;
   }
-  return slot.get();
+  return slot;
+}
+
+// A call that locked a workspace released meanwhile (its buffers are gone).
+int released_error() {
+  return fail(MER_ERR_RUNTIME_INVARIANT,
+              "the stream's workspace was released (mer_hip_stream_release / mer_hip_shutdown) while this call "
+              "waited for it; release must not overlap calls on that stream");
 }
 
 void free_workspace(Workspace &w) {
@@ -476,7 +492,10 @@ void bind_decode(DecodePlan &pl, float *f, uint32_t *counters, uint32_t *ctl, ui
 }
 
 // Grid sizing and the launch itself.
-int launch_planned(DecodePlan &pl, hipStream_t st) {
+// `prep`, if given, enqueues work on `st` that must run after the previous
+// decode launch of the device and before this one (the no-alloc scratch
+// preparation).
+int launch_planned(DecodePlan &pl, hipStream_t st, const std::function<hipError_t()> &prep = nullptr) {
   DeviceState &dev = g_dev[g_device.load()];
   DecodeParams &p = pl.p;
   const void *fn = decode_kernel_fn(pl.fmt, pl.gg.G, pl.gd.G);
@@ -496,18 +515,26 @@ int launch_planned(DecodePlan &pl, hipStream_t st) {
                 (unsigned long long)p.total_items);
 
   size_t tl = SIZE_MAX;
-  int trc = timing_begin(STAGE_DECODE, st, &tl);
-  if (trc) return trc;
-  uintptr_t expect = UINTPTR_MAX;
-  const uintptr_t me = reinterpret_cast<uintptr_t>(st);
-  const bool plain = dev.primary_stream.compare_exchange_strong(expect, me) || expect == me;
   hipError_t e;
   {
-    // Decode launches from different threads are issued one at a time:
-    // without this, cooperative launches concurrent with launches from other
-    // threads left the process to crash at exit (measured on ROCm 7).
     std::lock_guard<std::mutex> lk(g_launch_mu);
-    e = launch_decode(fn, (uint32_t)grid, p, st, !plain);
+    // Under graph capture the launch is not ordered here: the caller orders
+    // the graph's replays against decode calls on other streams.
+    const bool cap = capturing(st);
+    if (!cap && dev.decode_any && dev.decode_last != st) {
+      e = hipStreamWaitEvent(st, dev.decode_done, 0);
+      if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "ordering after the previous decode launch");
+    }
+    const int trc = timing_begin(STAGE_DECODE, st, &tl);
+    if (trc) return trc;
+    e = hipSuccess;
+    if (prep) e = prep();
+    if (e == hipSuccess) e = launch_decode(fn, (uint32_t)grid, p, st);
+    if (e == hipSuccess && !cap) {
+      e = hipEventRecord(dev.decode_done, st);
+      dev.decode_last = st;
+      dev.decode_any = true;
+    }
   }
   if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "decode launch");
   return timing_end(tl, st);
@@ -568,10 +595,10 @@ int run_decode_noalloc(int dtype, size_t dm, size_t dff, uint32_t n_tok, uint32_
   // shape: clear the exit count and abort flag, this call's counters and
   // release flags (one kernel, no memset node), and give a never-used epoch
   // word its first epoch.
-  hipError_t e = launch_decode_scratch_prep(ctl, 2 * kPollStride, counters,
-                                            (cnt_bytes + flag_bytes) / 4, pl.p.epoch_word, st);
-  if (e != hipSuccess) return hip_fail(e, MER_ERR_SUBMISSION, "no-alloc scratch preparation launch");
-  return launch_planned(pl, st);
+  return launch_planned(pl, st, [&] {
+    return launch_decode_scratch_prep(ctl, 2 * kPollStride, counters, (cnt_bytes + flag_bytes) / 4, pl.p.epoch_word,
+                                      st);
+  });
 }
 
 // Enqueue prep -> gate/up -> down -> combine for n_inst expert instances.
@@ -855,6 +882,10 @@ int mer_hip_init(int device) {
     if (e != hipSuccess || !ptr) return hip_fail(e, MER_ERR_RUNTIME_INVARIANT, "no-alloc scratch symbol address");
     g_dev[device].noalloc_scratch = ptr;
   }
+  if (!g_dev[device].decode_done) {
+    e = hipEventCreateWithFlags(&g_dev[device].decode_done, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_fail(e, MER_ERR_RUNTIME_INVARIANT, "decode ordering event");
+  }
   g_dev[device].ready = true;
   g_device = device;
   return ok();
@@ -869,6 +900,7 @@ int mer_hip_shutdown(void) {
   for (auto &kv : d.ws) {
     std::lock_guard<std::mutex> wl(kv.second->mu);
     free_workspace(*kv.second);
+    kv.second->released = true;
   }
   d.ws.clear();
   d.ready = false;
@@ -879,7 +911,7 @@ int mer_hip_shutdown(void) {
 int mer_hip_stream_release(void *stream) {
   int rc = require_init();
   if (rc) return rc;
-  std::unique_ptr<Workspace> w;
+  std::shared_ptr<Workspace> w;
   {
     std::lock_guard<std::mutex> lock(g_mu);
     auto &map = g_dev[g_device.load()].ws;
@@ -890,6 +922,7 @@ int mer_hip_stream_release(void *stream) {
   }
   std::lock_guard<std::mutex> wl(w->mu);  // waits for a call still enqueueing on it
   free_workspace(*w);
+  w->released = true;
   return MER_OK;
 }
 
@@ -1050,9 +1083,10 @@ int mer_hip_expert_forward(int dtype, const void *d_bytes, size_t len, const flo
     return e == hipSuccess ? MER_OK : hip_fail(e, MER_ERR_SUBMISSION, "zero output");
   }
   if (!d_bytes || !d_x || !d_y) return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
-  Workspace *w = workspace_for(st);
+  std::shared_ptr<Workspace> w = workspace_for(st);
   if (!w) return require_init();
   std::lock_guard<std::mutex> wl(w->mu);
+  if (w->released) return released_error();
   return run_experts(*w, dtype, d_model, d_ff, 1, 1, nullptr, 0, nullptr, (const uint8_t *)d_bytes, nullptr, d_x, d_y,
                      0u, true);
 }
@@ -1086,12 +1120,12 @@ int mer_hip_expert_forward_host(int dtype, const void *bytes, size_t len, const 
   if (e == hipSuccess) e = hipMemcpy(dx, x, d_model * sizeof(float), hipMemcpyHostToDevice);
   if (e != hipSuccess) rc = hip_fail(e, MER_ERR_UPLOAD, "host-to-device copy");
   if (!rc) {
-    Workspace *w = workspace_for(nullptr);
+    std::shared_ptr<Workspace> w = workspace_for(nullptr);
     if (!w) {
       rc = require_init();
     } else {
       std::lock_guard<std::mutex> wl(w->mu);
-      rc = run_experts(*w, dtype, d_model, d_ff, 1, 1, nullptr, 0, nullptr, (const uint8_t *)db, nullptr, dx, dy, 0u,
+      rc = w->released ? released_error() : run_experts(*w, dtype, d_model, d_ff, 1, 1, nullptr, 0, nullptr, (const uint8_t *)db, nullptr, dx, dy, 0u,
                        true);
     }
   }
@@ -1122,9 +1156,10 @@ int mer_hip_moe_forward(int dtype, size_t d_model, size_t d_ff, size_t n_tokens,
     return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "too many expert instances");
   if (!d_expert_table || !d_expert_ids || !d_weights || !d_x || !d_out)
     return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
-  Workspace *w = workspace_for((hipStream_t)stream);
+  std::shared_ptr<Workspace> w = workspace_for((hipStream_t)stream);
   if (!w) return require_init();
   std::lock_guard<std::mutex> wl(w->mu);
+  if (w->released) return released_error();
   return run_experts(*w, dtype, d_model, d_ff, (uint32_t)n_tokens, (uint32_t)top_k, d_expert_table,
                      (uint32_t)table_len, d_expert_ids, nullptr, d_weights, d_x, d_out, flags, false);
 }
@@ -1179,9 +1214,10 @@ int mer_hip_expert_batch_f16(int dtype, size_t d_model, size_t d_ff, size_t n_ex
   // Each expert is a one-slot token of weight 1 on its own copy of x, so
   // the routed forward's output row i is y of expert i, uncombined.
   const hipStream_t st = (hipStream_t)stream;
-  Workspace *w = workspace_for(st);
+  std::shared_ptr<Workspace> w = workspace_for(st);
   if (!w) return require_init();
   std::lock_guard<std::mutex> wl(w->mu);
+  if (w->released) return released_error();
   const size_t need = 2 * n_experts * d_model;
   rc = ensure_buf(*w, &w->stage, &w->stage_floats, need, 0, false, "f16 staging allocation");
   if (rc) return rc;
@@ -1219,9 +1255,10 @@ int mer_hip_moe_grouped(int dtype, size_t d_model, size_t d_ff, size_t n_tokens,
                 kMaxGroupedExperts, table_len);
   if (!d_expert_table || !d_expert_ids || !d_weights || !d_x || !d_out)
     return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
-  Workspace *w = workspace_for((hipStream_t)stream);
+  std::shared_ptr<Workspace> w = workspace_for((hipStream_t)stream);
   if (!w) return require_init();
   std::lock_guard<std::mutex> wl(w->mu);
+  if (w->released) return released_error();
   return run_grouped(*w, dtype, d_model, d_ff, (uint32_t)n_tokens, (uint32_t)top_k, d_expert_table,
                      (uint32_t)table_len, d_expert_ids, d_weights, d_x, d_out, flags);
 }
@@ -1256,9 +1293,10 @@ int mer_hip_moe_forward_layers(int dtype, size_t d_model, size_t d_ff, size_t n_
     la[l].x = a.x;
     la[l].out = a.out;
   }
-  Workspace *w = workspace_for((hipStream_t)stream);
+  std::shared_ptr<Workspace> w = workspace_for((hipStream_t)stream);
   if (!w) return require_init();
   std::lock_guard<std::mutex> wl(w->mu);
+  if (w->released) return released_error();
   return run_decode(*w, dtype, d_model, d_ff, (uint32_t)n_layers, (uint32_t)n_tokens, (uint32_t)top_k, la, nullptr,
                     flags);
 }
@@ -1305,12 +1343,13 @@ int mer_hip_route_linear_gate(const float *d_gate, size_t n_experts, size_t d_mo
     p.scaling = options->routed_scaling_factor;
   }
   p.logit_buf = d_logits;
-  Workspace *w = nullptr;
+  std::shared_ptr<Workspace> w;
   std::unique_lock<std::mutex> wl;
   if (!d_logits) {
     w = workspace_for((hipStream_t)stream);
     if (!w) return require_init();
     wl = std::unique_lock<std::mutex>(w->mu);
+    if (w->released) return released_error();
     rc = ensure_buf(*w, &w->router_buf, &w->router_floats, n_tokens * n_experts, 0, false, "router logits allocation");
     if (rc) return rc;
     p.logit_buf = w->router_buf;

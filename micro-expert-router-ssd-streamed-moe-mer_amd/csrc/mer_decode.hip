@@ -77,7 +77,7 @@ __device__ __forceinline__ const uint8_t *resolve_expert(const DecodeParams &p, 
   const uint64_t v = reinterpret_cast<const uint64_t *>(la.table)[id];
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return reinterpret_cast<const uint8_t *>(((uint64_t)hi << 32) | lo);
+  return reinterpret_cast<const uint8_t *>(join_u32(hi, lo));
 }
 
 // Wait for this wave's outstanding stores; keeps the compiler from moving
@@ -511,15 +511,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q
   // Every wave reads the launch's epoch; the word changes only after the
   // last wave has left (below).
   const uint64_t epoch_v = ld_dev(p.epoch_word);
-  const uint64_t epoch = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(epoch_v >> 32)) << 32) |
-                         __builtin_amdgcn_readfirstlane((uint32_t)epoch_v);
+  const uint64_t epoch = join_u32((uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(epoch_v >> 32)),
+                                  (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)epoch_v));
   // Item i goes to workgroup i mod grid.  An item waits only on items with
   // smaller indices.  The walk drains as long as no wave waits forever on an
-  // item of a workgroup that never becomes resident: a cooperative launch
-  // makes the whole grid resident at once, and a plain launch is used only
-  // where no other persistent grid of this library can overlap it, so its
-  // pending workgroups become resident as the kernels beside it finish
-  // (launch_decode and its caller).
+  // item of a workgroup that never becomes resident: the host orders all
+  // decode launches of a device one after another (launch_planned), so no
+  // other persistent grid of this library overlaps this one, and workgroups
+  // still pending behind other kernels become resident as those finish.
   for (uint32_t gi = blockIdx.x; gi < p.total_items; gi += gridDim.x) {
     TraceMarks tm{};
     tm.start = trace_now(p);
@@ -820,9 +819,8 @@ const void *decode_kernel_fn(int fmt, int gg, int gd) {
   return fmt == FMT_Q4_0 ? decode_fn_fmt<FMT_Q4_0>(gg, gd) : decode_fn_fmt<FMT_Q8_0>(gg, gd);
 }
 
-hipError_t launch_decode(const void *fn, uint32_t grid, const DecodeParams &p, hipStream_t st, bool cooperative) {
+hipError_t launch_decode(const void *fn, uint32_t grid, const DecodeParams &p, hipStream_t st) {
   void *args[] = {const_cast<DecodeParams *>(&p)};
-  if (cooperative) return hipLaunchCooperativeKernel(fn, dim3(grid), dim3(64), args, 0, st);
   return hipLaunchKernel(fn, dim3(grid), dim3(64), args, 0, st);
 }
 

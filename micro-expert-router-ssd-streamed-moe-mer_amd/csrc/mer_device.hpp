@@ -75,6 +75,12 @@ __host__ __device__ inline uint16_t f32_to_f16_bits(float f) {
   return (uint16_t)h;
 }
 
+// 64-bit value from two 32-bit halves.  Taking the halves as uint32_t
+// matters where they come from __builtin_amdgcn_readfirstlane, which returns
+// int: OR-ing that int into a 64-bit value would sign-extend a low half with
+// bit 31 set over the high half.
+__host__ __device__ constexpr uint64_t join_u32(uint32_t hi, uint32_t lo) { return ((uint64_t)hi << 32) | lo; }
+
 __device__ __forceinline__ uint32_t realign16(uint32_t lo, uint32_t hi) {
   // bytes 2..5 of the little-endian pair (lo, hi)
   return __builtin_amdgcn_alignbit(hi, lo, 16);

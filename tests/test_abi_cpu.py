@@ -146,3 +146,35 @@ def test_output_digest_matches_oracle_and_hand_case(mer, oracle):
     d, norm = mer.summarise_output(2, 5, np.array([1.0], np.float32))
     assert d == (((0xCBF29CE484222325 ^ 2 ^ 5) ^ 0x3F800000) * 0x100000001B3) % (1 << 64)
     assert norm == 1.0
+
+
+def test_join_u32_does_not_sign_extend(tmp_path):
+    """The kernels rebuild 64-bit values (launch epochs, blob pointers) from
+    two halves taken through __builtin_amdgcn_readfirstlane, which returns
+    int; mer::join_u32 takes the halves as uint32_t, so a low half with bit
+    31 set stays in the low 32 bits.  The helper is __host__ __device__ and
+    is checked here in a host build."""
+    import shutil
+    import subprocess
+
+    hipcc = "/opt/rocm/bin/hipcc" if os.path.exists("/opt/rocm/bin/hipcc") else shutil.which("hipcc")
+    if not hipcc:
+        pytest.skip("hipcc not available")
+    src = tmp_path / "join.hip"
+    src.write_text(
+        '#include "mer_device.hpp"\n'
+        "#include <stdio.h>\n"
+        "int main() {\n"
+        "  const int lo = (int)0x80000001u;  // what readfirstlane hands back\n"
+        "  const unsigned long long v = mer::join_u32(0x12345678u, (uint32_t)lo);\n"
+        "  static_assert(mer::join_u32(1u, 0x80000000u) == 0x180000000ull, \"join\");\n"
+        '  printf("%llx\\n", v);\n'
+        "  return v == 0x1234567880000001ull ? 0 : 1;\n"
+        "}\n")
+    exe = tmp_path / "join"
+    csrc = os.path.join(ROOT, "micro-expert-router-ssd-streamed-moe-mer_amd", "csrc")
+    r = subprocess.run([hipcc, "-std=c++17", "--offload-arch=gfx950", "-I", csrc, str(src), "-o", str(exe)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0 and out.stdout.strip() == "1234567880000001", out.stdout

@@ -9,9 +9,9 @@ through the C ABI at once, on the same resident experts; every output must
 be bit-identical to the serial run of the same call (scheduling never
 changes a sum's order) and within the 1e-3 bar of the oracle.  Four
 full-grid persistent decode launches on four streams cannot all be
-resident at once: the device's first decode stream launches plainly and
-every other stream cooperatively (a grid resident as a whole), so these
-cases also check that no two persistent grids stall each other.
+resident at once: the library orders every decode launch of the device
+after the previous one, whatever its stream, so these cases also check
+that no two persistent grids stall each other.
 """
 from __future__ import annotations
 

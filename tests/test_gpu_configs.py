@@ -57,6 +57,39 @@ def test_qwen3_layers_chained(mer, oracle, gpu):
     del tables
 
 
+def test_qwen3_layers_chained_at_config_scale(mer, oracle, gpu):
+    """The chained-residual decode at BASELINE config 2's own weight scales
+    (Q8_0 d ~ U(0.002, 0.01), x ~ N(0,1)): three layers of x <- x + moe(x)
+    in one launch.  Without the model's RMSNorm between layers (not part of
+    the expert FFN) the hidden state grows by orders of magnitude per layer
+    (about 2e4, 2e12, 5e27 here); three layers stay finite in f32, and the
+    combined bar of assert_ffn_close scales its absolute floor with them."""
+    dm, dff, n_layers, n_exp, k = 2048, 768, 3, 16, 8
+    say("qwen3 3 chained layers at config-2 scales")
+    blobs = [[make_expert(oracle, Q8, dm, dff, 700 + l * n_exp + e) for e in range(n_exp)] for l in range(n_layers)]
+    tables = [_table(b, gpu) for b in blobs]
+    rng = np.random.default_rng(15)
+    x0 = rng.standard_normal((1, dm)).astype(np.float32)
+    ids, ws, want, xin = [], [], [], x0
+    for l in range(n_layers):
+        ids.append(np.stack([rng.choice(n_exp, k, replace=False)]).astype(np.int32))
+        ws.append((rng.random((1, k)) + 0.1).astype(np.float32))
+        out = xin + _oracle_moe(oracle, Q8, blobs[l], ids[l], ws[l], xin, dm, dff)
+        assert np.isfinite(out).all(), f"reference layer {l} overflowed"
+        say(f"layer {l}: max|out| {np.abs(out).max():.3g}")
+        want.append(out)
+        xin = out
+    layers = [dict(table=tables[l][1], ids=to_dev(ids[l], gpu), weights=to_dev(ws[l], gpu),
+                   x=to_dev(x0, gpu) if l == 0 else None, out=torch.zeros((1, dm), device=gpu))
+              for l in range(n_layers)]
+    mer.moe_forward_layers(mer.WeightDtype.Q8_0, dm, dff, layers, residual=True, chain=True)
+    torch.cuda.synchronize()
+    for l in range(n_layers):
+        assert_ffn_close(layers[l]["out"].cpu().numpy(), want[l], f"chained config-2 layer {l}")
+    mer.take_device_status()
+    del tables
+
+
 def test_deepseek_cache_pressure_steps(mer, oracle, gpu):
     """DeepSeek-V3-shaped routed experts (d_model 7168, d_ff 2048, Q4_0),
     decode batch 4 x top-8 through a VRAM slot cache holding fewer slots
@@ -87,6 +120,91 @@ def test_deepseek_cache_pressure_steps(mer, oracle, gpu):
         want = _oracle_moe(oracle, Q4, blobs, ids, w, x, dm, dff)
         assert_ffn_close(out.cpu().numpy(), want, f"step {s}")
     assert cache.stats()["misses"] > 0
+    cache.close()
+
+
+def _lru_model(n_slots, batches):
+    """Host model of the slot cache's accounting (expert_cache.rs:715-1350
+    admission, LRU victim among slots the call does not need): per prepare,
+    already-resident ids are hits, the others misses, each miss into a full
+    cache evicts the least recently used unneeded expert."""
+    last, tick = {}, 0
+    hits = misses = evictions = 0
+    for distinct in batches:
+        needed = set()
+        for e in distinct:
+            if e in last:
+                hits += 1
+                tick += 1
+                last[e] = tick
+                needed.add(e)
+        for e in distinct:
+            if e in needed:
+                continue
+            if len(last) >= n_slots:
+                victim = min((v for v in last if v not in needed), key=last.get)
+                del last[victim]
+                evictions += 1
+            tick += 1
+            last[e] = tick
+            needed.add(e)
+            misses += 1
+    return hits, misses, evictions
+
+
+def test_deepseek_config4_cache_ratio(mer, oracle, gpu):
+    """BASELINE config 4 at its own cache ratio: 25% of the experts fit in
+    VRAM (16 slots over 64 DeepSeek-V3-shaped Q4_0 experts), decode batch
+    4 x top-8 drawn from SkewedStream(Zipf 1.0, stay 0.7) (workload.rs:
+    54-175), six steps with evictions.  A step whose tokens need more
+    distinct experts than the cache holds runs as consecutive token groups
+    that each fit, as an engine bounded by its slots must.  Outputs are
+    checked against the oracle and the hit / miss / eviction counters
+    against a host model of the cache's LRU admission."""
+    dm, dff, n_exp, n_slots, T, k, n_steps = 7168, 2048, 64, 16, 4, 8, 6
+    say("deepseek config 4: 16 slots over 64 experts")
+    blobs = [make_expert(oracle, Q4, dm, dff, 500 + e) for e in range(n_exp)]
+    host = []
+    for b in blobs:
+        t = torch.empty(b.size, dtype=torch.uint8, pin_memory=True)
+        t.copy_(torch.from_numpy(b))
+        host.append(t)
+    stream = routing.SkewedStream(n_exp, k, 1.0, 0.7, 4)
+    cache = mer.SlotCache(mer.WeightDtype.Q4_0, dm, dff, n_slots, n_exp)
+    rng = np.random.default_rng(12)
+    runs, batches = [], []
+    for s in range(n_steps):
+        ids = np.array([stream.next_experts() for _ in range(T)], np.int32)
+        w = rng.random((T, k)).astype(np.float32)
+        x = rng.standard_normal((T, dm)).astype(np.float32)
+        groups, cur = [], []
+        for t in range(T):  # token groups whose distinct experts fit the slots
+            union = set(int(v) for v in ids[cur + [t]].reshape(-1))
+            if cur and len(union) > n_slots:
+                groups.append(cur)
+                cur = []
+            cur.append(t)
+        groups.append(cur)
+        for g in groups:
+            distinct = list(dict.fromkeys(int(v) for v in ids[g].reshape(-1)))
+            batches.append(distinct)
+            cache.prepare(distinct, host_blobs=[host[e] for e in distinct])
+            out = mer.moe_forward(mer.WeightDtype.Q4_0, dm, dff, cache, to_dev(ids[g], gpu), to_dev(w[g], gpu),
+                                  to_dev(x[g], gpu))
+            runs.append((s, ids[g], w[g], x[g], out))
+    torch.cuda.synchronize()
+    mer.take_device_status()
+    for i, (s, ids, w, x, out) in enumerate(runs):
+        want = _oracle_moe(oracle, Q4, blobs, ids, w, x, dm, dff)
+        assert_ffn_close(out.cpu().numpy(), want, f"step {s} group {i}")
+    st = cache.stats()
+    hits, misses, evictions = _lru_model(n_slots, batches)
+    say(f"config 4 cache: {len(batches)} prepares, hits {st['hits']} misses {st['misses']} "
+        f"evictions {st['evictions']}")
+    assert (st["hits"], st["misses"], st["evictions"]) == (hits, misses, evictions)
+    assert st["evictions"] > 0 and st["hits"] > 0
+    assert st["resident"] == n_slots
+    assert st["bytes_uploaded"] == misses * mer.expert_weight_bytes_for(dm, dff, mer.WeightDtype.Q4_0)
     cache.close()
 
 

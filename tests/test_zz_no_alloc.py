@@ -15,11 +15,12 @@ from test_gpu_parity import Q4, Q8, _oracle_moe, _table, assert_ffn_close, make_
 pytestmark = pytest.mark.gpu
 
 
-def _call(mer, name, dtype, dm, dff, table, n_exp, ids, w, x, out, flags):
+def _call(mer, name, dtype, dm, dff, table, n_exp, ids, w, x, out, flags, stream=None):
     lib = mer._lib.lib()
     n_tok, k = ids.shape
+    st = (stream or torch.cuda.current_stream()).cuda_stream
     return getattr(lib, name)(dtype, dm, dff, n_tok, k, table.data_ptr(), n_exp, ids.data_ptr(), w.data_ptr(),
-                              x.data_ptr(), out.data_ptr(), flags, torch.cuda.current_stream().cuda_stream)
+                              x.data_ptr(), out.data_ptr(), flags, st)
 
 
 def test_noalloc_matches_moe_forward(mer, oracle, gpu):
@@ -63,3 +64,44 @@ def test_noalloc_rejects_oversized_and_unaligned(mer, oracle, gpu):
     rc = lib.mer_hip_moe_forward_noalloc(Q4, 96, 160, 1, 1, dummy.data_ptr(), 16, dummy.data_ptr(),
                                          dummy.data_ptr(), dummy.data_ptr(), dummy.data_ptr(), 0, 0)
     assert rc == 4 and "multiples of 64" in mer._lib.last_error()[1]
+
+
+def test_noalloc_two_streams_back_to_back(mer, oracle, gpu):
+    """Two streams issue no-alloc calls back to back with no host
+    synchronisation in between, on different inputs and shapes: the calls
+    share the GPU's one scratch array, and the library orders every decode
+    launch of a device after the previous one, so each output must equal
+    mer_hip_moe_forward's bit for bit."""
+    say("noalloc on two streams")
+    cases = [(Q4, 1024, 2048, 2, 2), (Q4, 512, 1024, 1, 2)]
+    runs = []
+    for i, (dtype, dm, dff, n_tok, k) in enumerate(cases):
+        n_exp = 4
+        blobs = [make_expert(oracle, dtype, dm, dff, 400 + 10 * i + e) for e in range(n_exp)]
+        devs, table = _table(blobs, gpu)
+        calls = []
+        for c in range(3):
+            rng = np.random.default_rng(90 + 10 * i + c)
+            ids = np.stack([rng.choice(n_exp, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
+            w = rng.random((n_tok, k)).astype(np.float32)
+            x = rng.standard_normal((n_tok, dm)).astype(np.float32)
+            ids_d, w_d, x_d = to_dev(ids, gpu), to_dev(w, gpu), to_dev(x, gpu)
+            ref = torch.zeros((n_tok, dm), device=gpu)
+            assert _call(mer, "mer_hip_moe_forward", dtype, dm, dff, table, n_exp, ids_d, w_d, x_d, ref, 0) == 0
+            calls.append((ids_d, w_d, x_d, ref, torch.full((n_tok, dm), float("nan"), device=gpu)))
+        runs.append((dtype, dm, dff, n_exp, devs, table, calls))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device=gpu) for _ in range(2)]
+    for c in range(3):  # interleave: stream 0 runs case 0, stream 1 case 1, no host sync
+        for s_idx, (dtype, dm, dff, n_exp, devs, table, calls) in enumerate(runs):
+            ids_d, w_d, x_d, ref, got = calls[c]
+            rc = _call(mer, "mer_hip_moe_forward_noalloc", dtype, dm, dff, table, n_exp, ids_d, w_d, x_d, got, 0,
+                       stream=streams[s_idx])
+            assert rc == 0, mer._lib.last_error()
+    torch.cuda.synchronize()
+    for s_idx, (dtype, dm, dff, n_exp, devs, table, calls) in enumerate(runs):
+        for c, (_, _, _, ref, got) in enumerate(calls):
+            assert np.array_equal(got.cpu().numpy(), ref.cpu().numpy()), f"stream {s_idx} call {c}"
+    mer.take_device_status()
+    for s in streams:
+        mer.stream_release(s)
