@@ -646,6 +646,40 @@ def main() -> int:
             "ms_per_step": (r1 - r0) * 1e3 / args.steps, "avg_launch_us": rap_us,
             "frac": launch_bytes / (rap_us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
             "note": "the same steps with MER_MOE_ROUTE_AFTER_PREV (routing known only after the previous layer)"}
+    if args.config in (1, 2) and not args.per_layer and not args.route_after_prev and not args.no_route_after_prev_pass:
+        # The same steps as one mer_hip_moe_forward call per layer, MER's own
+        # call pattern (moe_step_inner's WeightedInto, engine.rs:5206,
+        # :5548-5639): each call reads its layer's routing and input when the
+        # stream reaches it, after the previous layer's call has finished.
+        pl_fn = lib.mer_hip_moe_forward
+        pl_args = [[(dtype, dm, dff, 1, K, table[l].data_ptr(), E, ids_d[s, l].data_ptr(), wts_d[s, l].data_ptr(),
+                     xsel(s, l).data_ptr(), outs[s].data_ptr(), 2, stream) for l in range(L)]
+                   for s in range(total_steps)]
+        for s in range(args.warmup):
+            for a in pl_args[s]:
+                pl_fn(*a)
+        mer.stage_timing_enable(True)
+        torch.cuda.synchronize()
+        p0 = time.perf_counter()
+        for s in range(args.warmup, total_steps):
+            for a in pl_args[s]:
+                rc = pl_fn(*a)
+                if rc:
+                    mer.errors.raise_for_status(rc)
+        torch.cuda.synchronize()
+        p1 = time.perf_counter()
+        pl_stage = mer.stage_timing_read()["decode"]
+        mer.stage_timing_enable(False)
+        mer.take_device_status()
+        pl_us = pl_stage[0] / max(pl_stage[1], 1) * 1e3
+        pl_ms = (p1 - p0) * 1e3 / args.steps
+        result["per_layer"] = {
+            "value": args.steps / (p1 - p0) * cfg.get("tokens", 1), "unit": cfg["unit"],
+            "ms_per_step": pl_ms, "launches_per_step": L, "avg_launch_us": pl_us,
+            "frac": step_bytes / (pl_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+            "kernel_frac": per_layer_bytes / (pl_us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+            "note": "the same steps as one mer_hip_moe_forward per layer (MER's call pattern); frac counts the "
+                    "whole step (launch gaps included), kernel_frac the average launch"}
     if args.config == 2:
         result["router"] = router_pass(gates, xs_d, ids, L, E, K, dm, args.warmup, min(5, args.steps))
     traffic = read_traffic(args.config) if dominant == "decode" and not args.per_layer else None

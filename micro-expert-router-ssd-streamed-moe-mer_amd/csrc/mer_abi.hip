@@ -89,9 +89,8 @@ struct Workspace {
   size_t release_words = 0;
 };
 
-// Control lines at the end of a workspace's counter allocation, one
-// 256-byte line each: exit count, abort flag, launch epoch.
-constexpr size_t kCtlLines = 3;
+// Control lines (kCtlLines, mer_internal.hpp) sit at the end of a
+// workspace's counter allocation.
 
 struct DeviceState {
   bool ready = false;
@@ -276,7 +275,7 @@ int ensure_counters(Workspace &w, size_t words, uint32_t **out) {
   if (grow) {
     const uint64_t first = ++g_host_epoch;
     uint32_t *ctl = w.counters + w.counter_words - kCtlLines * kPollStride;
-    hipError_t e = hipMemcpyAsync(ctl + 2 * kPollStride, &first, sizeof first, hipMemcpyHostToDevice, w.stream);
+    hipError_t e = hipMemcpyAsync(ctl + kCtlEpochLine * kPollStride, &first, sizeof first, hipMemcpyHostToDevice, w.stream);
     if (e == hipSuccess) e = hipStreamSynchronize(w.stream);
     if (e != hipSuccess) return hip_fail(e, MER_ERR_PHYSICAL_CAPACITY, "decode counter initialisation");
   }
@@ -488,7 +487,8 @@ void bind_decode(DecodePlan &pl, float *f, uint32_t *counters, uint32_t *ctl, ui
   p.gd_release = pl.gd_fan ? release + pl.layer_flags : nullptr;
   p.exit_count = ctl;
   p.abort_flag = ctl + kPollStride;
-  p.epoch_word = reinterpret_cast<uint64_t *>(ctl + 2 * kPollStride);
+  p.exit_groups = ctl + 2 * kPollStride;
+  p.epoch_word = reinterpret_cast<uint64_t *>(ctl + kCtlEpochLine * kPollStride);
 }
 
 // Grid sizing and the launch itself.
@@ -562,9 +562,10 @@ int run_decode(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_layers
 // per device, held until the process ends.  In host code `scratch` names a
 // host-side stand-in; the device address comes from hipGetSymbolAddress
 // (DeviceState::noalloc_scratch), which is what kernels and copies use.
-// Layout: [0, 768) exit count, abort flag and epoch word (a 256-byte line
-// each, at fixed offsets so the epoch word survives calls of any shape),
-// then the counters, the release flags and the float region of the call.
+// Layout: the kCtlLines control lines (exit count, abort flag, exit-group
+// counters, epoch word: a 256-byte line each, at fixed offsets so the epoch
+// word survives calls of any shape), then the counters, the release flags
+// and the float region of the call.
 constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
@@ -577,7 +578,7 @@ int run_decode_noalloc(int dtype, size_t dm, size_t dff, uint32_t n_tok, uint32_
   plan_decode(pl, dtype, dm, dff, 1, n_tok, top_k, &la, nullptr, flags);
   auto up256 = [](size_t b) { return (b + 255) / 256 * 256; };
   const size_t ctl_bytes = kCtlLines * kPollStride * 4;
-  const size_t cnt_bytes = up256(pl.p.n_counters * 4);
+  const size_t cnt_bytes = up256((pl.p.n_counters) * 4);
   const size_t flag_bytes = up256((pl.layer_flags + pl.gd_flags) * 8);
   const size_t float_bytes = up256(pl.floats() * 4);
   const size_t need = ctl_bytes + cnt_bytes + flag_bytes + float_bytes;
@@ -596,7 +597,7 @@ int run_decode_noalloc(int dtype, size_t dm, size_t dff, uint32_t n_tok, uint32_
   // release flags (one kernel, no memset node), and give a never-used epoch
   // word its first epoch.
   return launch_planned(pl, st, [&] {
-    return launch_decode_scratch_prep(ctl, 2 * kPollStride, counters, (cnt_bytes + flag_bytes) / 4, pl.p.epoch_word,
+    return launch_decode_scratch_prep(ctl, kCtlEpochLine * kPollStride, counters, (cnt_bytes + flag_bytes) / 4, pl.p.epoch_word,
                                       st);
   });
 }

@@ -760,7 +760,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q
   // and gives the next launch on
   // this workspace a fresh epoch, unique on the device: the top bit set
   // keeps it apart from the host-chosen first epochs of workspaces.
-  if (arrive_last(p.exit_count, gridDim.x)) {
+  const uint32_t grp = blockIdx.x % kExitGroups;
+  const uint32_t in_grp = gridDim.x / kExitGroups + (grp < gridDim.x % kExitGroups ? 1u : 0u);
+  uint32_t *grp_ctr = p.exit_groups + (size_t)grp * kPollStride;
+  if (!arrive_last(grp_ctr, in_grp)) return;
+  if (lane == 0) st_dev(grp_ctr, 0u);  // ready for the next launch (drained by the arrival below)
+  if (arrive_last(p.exit_count, min(gridDim.x, kExitGroups))) {
     for (uint32_t i = lane; i < p.n_counters; i += 64) st_dev(p.counters + i, 0u);
     if (lane == 0) {
       st_dev(p.abort_flag, 0u);
@@ -774,7 +779,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q
 
 // Prepares decode scratch whose earlier contents belong to calls of other
 // shapes (the no-alloc entry point's static array): zeroes n_ctl words at
-// ctl (exit count, abort flag) and n_zero words at zero (counters, release
+// ctl (exit count, abort flag, exit-group counters) and n_zero words at zero (counters, release
 // flags), and gives an epoch word that has never been used (0) its first
 // epoch.
 __global__ __launch_bounds__(256) void decode_scratch_prep_kernel(uint32_t *ctl, uint32_t n_ctl, uint32_t *zero,

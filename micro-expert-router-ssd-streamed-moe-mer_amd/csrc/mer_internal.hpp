@@ -93,6 +93,15 @@ constexpr uint32_t kPollStride = 64;     // words between polled decode counters
 constexpr uint32_t kFlagStride = 32;     // 64-bit release flags between polled flags (one 256-byte line each)
 constexpr uint32_t kReleaseFan = 16;     // release flags per (layer, token), one line each
 constexpr uint32_t kCombineBatch = 16;   // partial sums a decode combine loads in one batch
+// Control lines of a decode workspace (one 256-byte line each): exit count,
+// abort flag, kExitGroups exit-group counters, then the launch epoch word.
+// Waves leave through a two-level count (a group counter, then the exit
+// count for the last wave of each group): device-scope atomics on one
+// address are serialised, ~20 ns each, so 3072 exits on one counter would
+// take ~60 us.
+constexpr uint32_t kExitGroups = 64;
+constexpr uint32_t kCtlEpochLine = 2 + kExitGroups;
+constexpr uint32_t kCtlLines = 3 + kExitGroups;
 
 struct LayerArgs {
   const void *const *table;  // device array of expert blob pointers
@@ -136,6 +145,7 @@ struct DecodeParams {
   uint64_t *release;         // [L][n_tok][kReleaseFan] epoch flags (never cleared: other epochs read as not set)
   uint64_t *gd_release;      // [L][n_inst][d_slices][kReleaseFan] h-slice release flags, or null (counters)
   uint32_t *exit_count;
+  uint32_t *exit_groups;      // kExitGroups counters, kPollStride words apart
   uint32_t *abort_flag;      // set by a timed-out wait; later waits give up
   uint32_t *status;
   uint64_t timeout_ticks;
