@@ -97,7 +97,7 @@ struct DeviceState {
   int cus = 256;
   uint32_t *status = nullptr;
   uint64_t clock_khz = 100000;
-  std::atomic<int> occupancy[2][3][3] = {};  // resident decode workgroups per CU, by (fmt, GG, GD)
+  std::atomic<int> occupancy[2][2][3][3] = {};  // resident decode workgroups per CU, by (pair, fmt, GG, GD)
   // Device-wide order of persistent decode launches (guarded by
   // g_launch_mu).  The decode grid fills the device and hands items out by
   // static stride, so it needs all of its workgroups resident; two such
@@ -379,6 +379,7 @@ struct DecodePlan {
   DecodeParams p;
   int fmt;
   SliceGeom gg, gd;
+  bool pair;  // two-wave workgroups: a tile's two gate/up slices add up in LDS
   size_t n_xd, n_gp, n_hd, n_pa;  // floats: x digit lines, gate/up slice partials, h digit lines, down partials
   size_t layer_flags, gd_flags;   // 64-bit release flags
   bool gd_fan;
@@ -432,9 +433,21 @@ void plan_decode(DecodePlan &pl, int dtype, size_t dm, size_t dff, uint32_t n_la
   p.p_items = (uint32_t)div_ceil(p.xblocks, pack_blocks);
   p.combine_packs = 1u;
   p.off_p = n_tok;
+  // Gate/up rows cut into two slices of at most 32 chunks run in two-wave
+  // workgroups (items 2u and 2u+1 of one unit): the slices of a tile are
+  // consecutive items, so with the G items starting at an even index of an
+  // even-length layer they always share a workgroup and add up in LDS.
+  // Measured: MER_DECODE_NO_PAIR=1 keeps the one-wave layout (A/B).
+  static const bool no_pair = [] {
+    const char *v = getenv("MER_DECODE_NO_PAIR");
+    return v && v[0] == '1';
+  }();
+  pl.pair = !no_pair && pl.gg.slices == 2 && pl.gg.G <= 32;
   p.off_g = p.off_p + n_tok * p.p_items;
+  if (pl.pair && (p.off_g & 1u)) ++p.off_g;  // one padding P item
   p.off_d = p.off_g + p.n_inst * p.g_slices * p.g_tiles;
   p.items_per_layer = p.off_d + p.n_inst * p.d_slices * p.d_tiles;
+  if (pl.pair && (p.items_per_layer & 1u)) ++p.items_per_layer;  // one padding D item
   p.total_items = (uint64_t)p.items_per_layer * n_layers;
 
   // counters per layer.  Polled counters (P[n_tok] G-done[n_inst*d_slices]
@@ -452,7 +465,7 @@ void plan_decode(DecodePlan &pl, int dtype, size_t dm, size_t dff, uint32_t n_la
   auto up64 = [](size_t v) { return (v + 63) / 64 * 64; };
   const size_t L = n_layers;
   pl.n_xd = L * n_tok * p.xblocks * kLineDwords;
-  pl.n_gp = p.g_slices > 1 ? up64(L * p.n_inst * p.g_slices * 2 * dff) : 0;
+  pl.n_gp = p.g_slices > 1 && !pl.pair ? up64(L * p.n_inst * p.g_slices * 2 * dff) : 0;
   pl.n_hd = L * p.n_inst * p.hblocks * kLineDwords;
   pl.n_pa = up64(L * p.n_inst * p.d_slices * dm);
   // Release flags of layers, and of h slices when their count is small
@@ -498,19 +511,21 @@ void bind_decode(DecodePlan &pl, float *f, uint32_t *counters, uint32_t *ctl, ui
 int launch_planned(DecodePlan &pl, hipStream_t st, const std::function<hipError_t()> &prep = nullptr) {
   DeviceState &dev = g_dev[g_device.load()];
   DecodeParams &p = pl.p;
-  const void *fn = decode_kernel_fn(pl.fmt, pl.gg.G, pl.gd.G);
-  std::atomic<int> &occ_slot = dev.occupancy[pl.fmt][g_index(pl.gg.G)][g_index(pl.gd.G)];
+  const void *fn = decode_kernel_fn(pl.fmt, pl.gg.G, pl.gd.G, pl.pair);
+  const uint32_t wpg = pl.pair ? 2u : 1u;
+  std::atomic<int> &occ_slot = dev.occupancy[pl.pair][pl.fmt][g_index(pl.gg.G)][g_index(pl.gd.G)];
   int occ = occ_slot.load();
   if (occ == 0) {
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 64, 0);
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 64 * wpg, 0);
     if (e != hipSuccess || occ <= 0) return hip_fail(e, MER_ERR_RUNTIME_INVARIANT, "decode kernel occupancy query");
     occ_slot.store(occ);
   }
+  const uint64_t units = (p.total_items + wpg - 1) / wpg;
   uint64_t grid = (uint64_t)dev.cus * (uint64_t)occ;
-  if (grid > p.total_items) grid = p.total_items;
+  if (grid > units) grid = units;
   if (grid == 0) return MER_OK;
-  // item indices run to total_items + grid (each workgroup steps once past the end)
-  if (p.total_items + grid >= (uint64_t)UINT32_MAX)
+  // unit indices run to units + grid (each workgroup steps once past the end)
+  if ((units + grid) * wpg >= (uint64_t)UINT32_MAX)
     return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "decode launch of %llu items exceeds the 32-bit item space",
                 (unsigned long long)p.total_items);
 
@@ -529,7 +544,7 @@ int launch_planned(DecodePlan &pl, hipStream_t st, const std::function<hipError_
     if (trc) return trc;
     e = hipSuccess;
     if (prep) e = prep();
-    if (e == hipSuccess) e = launch_decode(fn, (uint32_t)grid, p, st);
+    if (e == hipSuccess) e = launch_decode(fn, (uint32_t)grid, wpg, p, st);
     if (e == hipSuccess && !cap) {
       e = hipEventRecord(dev.decode_done, st);
       dev.decode_last = st;

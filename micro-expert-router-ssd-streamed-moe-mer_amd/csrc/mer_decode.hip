@@ -84,6 +84,12 @@ __device__ __forceinline__ const uint8_t *resolve_expert(const DecodeParams &p, 
 // memory accesses across it.
 __device__ __forceinline__ void drain_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+// LDS written by some lanes of this wave, read by others: wait for the
+// wave's LDS accesses (a wave's LDS instructions complete in order).
+__device__ __forceinline__ void wave_lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+}
 
 __device__ __forceinline__ void set_status(const DecodeParams &p, uint32_t code) {
   atomicCAS(p.status, 0u, code);
@@ -495,10 +501,20 @@ __device__ __forceinline__ void fetch_digits(const uint32_t *dig, size_t block0,
 
 }  // namespace
 
-template <int FMT, int GG, int GD>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q4_0 ? 3 : 2))) void decode_kernel(DecodeParams p) {
-  __shared__ float s_h[kTileRows];
-  __shared__ float s_gu[2 * kTileRows];  // gate and up row sums of a single-slice G item
+// PAIR: workgroups of two waves taking items 2u and 2u+1 of unit u.  Used
+// when gate/up rows are cut into two column slices (narrow layers, single
+// experts): the slices of a tile are consecutive items, so they meet in one
+// workgroup and their partial sums are added in LDS instead of going
+// through memory and an arrival count (one round trip instead of three).
+template <int FMT, int GG, int GD, bool PAIR>
+__global__ __launch_bounds__(PAIR ? 128 : 64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q4_0 ? 3 : 2))) void decode_kernel(DecodeParams p) {
+  constexpr uint32_t kW = PAIR ? 2 : 1;  // waves per workgroup
+  const uint32_t wv = PAIR ? (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / 64) : 0u;
+  __shared__ float s_h_all[kW][kTileRows];
+  __shared__ float s_gu_all[kW][2 * kTileRows];  // gate and up row sums of a single-slice G item
+  __shared__ float s_pair[PAIR ? 2 : 1][2 * kTileRows];  // a paired G tile's slice sums
+  float *s_h = s_h_all[wv];
+  float *s_gu = s_gu_all[wv];
   const uint32_t lane = lane_id();
   using D = DigitTraits<FMT>;
   constexpr uint32_t kPackBlocks = 64 / D::kGroups;
@@ -519,7 +535,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q
   // decode launches of a device one after another (launch_planned), so no
   // other persistent grid of this library overlaps this one, and workgroups
   // still pending behind other kernels become resident as those finish.
-  for (uint32_t gi = blockIdx.x; gi < p.total_items; gi += gridDim.x) {
+  const uint64_t n_units = (p.total_items + kW - 1) / kW;
+  for (uint32_t u = blockIdx.x; u < n_units; u += gridDim.x) {
+    const uint32_t gi = u * kW + wv;
+    if (gi >= p.total_items) continue;  // the other wave of a last, odd unit
     TraceMarks tm{};
     tm.start = trace_now(p);
     const uint32_t l = (uint32_t)(gi / p.items_per_layer);
@@ -572,7 +591,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q
       const uint32_t idx = j - p.off_p;
       const uint32_t t = idx / p.p_items;
       const uint32_t part = idx % p.p_items;
-      if (l == 0 || !p.combine_packs) {  // else packed by layer l-1's combines
+      if (t < p.n_tok && (l == 0 || !p.combine_packs)) {  // else packed by layer l-1's combines (or padding)
         wait_prev_layer(t);  // layers run in order: layer l reads after layer l-1 wrote
         tm.ready = trace_now(p);
         const uint32_t b0 = part * kPackBlocks;
@@ -615,6 +634,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q
       auto emit = [&](bool writer, uint32_t r, int s, float a) {
         if (writer) {
           if (single_slice) s_gu[s * kTileRows + r - tile * kTileRows] = a;
+          else if (PAIR) s_pair[wv][s * kTileRows + r - tile * kTileRows] = a;
           else st_dev(gpart + (size_t)s * p.d_ff + r, a);
         }
       };
@@ -623,8 +643,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q
       tm.walked = trace_now(p);
       bool pack = single_slice;
       if (single_slice) {
-        __syncthreads();
+        wave_lds_sync();
         if (lane < kTileRows) s_h[lane] = expert ? silu_mul(s_gu[lane], s_gu[kTileRows + lane], p.swiglu_limit) : 0.f;
+      } else if (PAIR) {
+        // both waves of the workgroup hold the two slices of this tile
+        __syncthreads();
+        pack = wv == 0;
+        if (pack && lane < kTileRows)
+          s_h[lane] = expert ? silu_mul(s_pair[0][lane] + s_pair[1][lane],
+                                        s_pair[0][kTileRows + lane] + s_pair[1][kTileRows + lane], p.swiglu_limit)
+                             : 0.f;
+        __syncthreads();  // s_pair is free for the next unit
       } else {
         pack = arrive_last(cnt + p.c_ga + (size_t)inst * p.g_tiles + tile, p.g_slices);
         if (pack && lane < kTileRows) {
@@ -639,7 +668,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q
         }
       }
       if (pack) {
-        __syncthreads();
+        wave_lds_sync();
         const size_t hb = (size_t)inst * p.hblocks + tile;
         pack_blocks<FMT, false>(s_h, 1, hq_dig + hb * kLineDwords, epoch);
         uint32_t *gd = cnt + p.c_gd + ((size_t)inst * p.d_slices + dslice) * kPollStride;
@@ -654,6 +683,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q
     } else {
       // ---- D: down of one (slot, column slice, tile) + combine -------------
       const uint32_t idx = j - p.off_d;
+      if (idx >= p.n_inst * p.d_slices * p.d_tiles) continue;  // padding item
       const uint32_t per_tok = p.d_tiles * p.top_k * p.d_slices;
       const uint32_t t = idx / per_tok;
       const uint32_t rem = idx % per_tok;
@@ -696,7 +726,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q
       walk.run(wbuf, xd, xsc, emit);
       prio_hi();
       tm.walked = trace_now(p);
-      __syncthreads();
+      wave_lds_sync();
       // What a combine of this tile adds to the sum is already final: the
       // residual or accumulated output (written by layer l-1, complete before
       // any item of this layer ran) and the caller's next-layer input.  Every
@@ -742,7 +772,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q
         if (pack_next) {
           // block `tile` of layer l+1's input, the tile just combined (chained)
           // or the caller's next input, into layer l+1's digit lines
-          __syncthreads();
+          wave_lds_sync();
           uint32_t *next_dig = p.xq_dig + ((size_t)(l + 1) * p.n_tok * p.xblocks + (size_t)t * p.xblocks + tile) * kLineDwords;
           pack_blocks<FMT, false>(s_h, 1, next_dig, epoch);
         }
@@ -760,12 +790,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q
   // and gives the next launch on
   // this workspace a fresh epoch, unique on the device: the top bit set
   // keeps it apart from the host-chosen first epochs of workspaces.
-  const uint32_t grp = blockIdx.x % kExitGroups;
-  const uint32_t in_grp = gridDim.x / kExitGroups + (grp < gridDim.x % kExitGroups ? 1u : 0u);
+  const uint32_t n_waves = gridDim.x * kW;
+  const uint32_t grp = (blockIdx.x * kW + wv) % kExitGroups;
+  const uint32_t in_grp = n_waves / kExitGroups + (grp < n_waves % kExitGroups ? 1u : 0u);
   uint32_t *grp_ctr = p.exit_groups + (size_t)grp * kPollStride;
   if (!arrive_last(grp_ctr, in_grp)) return;
   if (lane == 0) st_dev(grp_ctr, 0u);  // ready for the next launch (drained by the arrival below)
-  if (arrive_last(p.exit_count, min(gridDim.x, kExitGroups))) {
+  if (arrive_last(p.exit_count, min(n_waves, kExitGroups))) {
     for (uint32_t i = lane; i < p.n_counters; i += 64) st_dev(p.counters + i, 0u);
     if (lane == 0) {
       st_dev(p.abort_flag, 0u);
@@ -801,32 +832,36 @@ hipError_t launch_decode_scratch_prep(uint32_t *ctl, uint32_t n_ctl, uint32_t *z
   return hipGetLastError();
 }
 
-template <int FMT, int GG, int GD>
+template <int FMT, int GG, int GD, bool PAIR>
 static const void *decode_fn() {
-  return reinterpret_cast<const void *>(&decode_kernel<FMT, GG, GD>);
+  return reinterpret_cast<const void *>(&decode_kernel<FMT, GG, GD, PAIR>);
 }
 
-template <int FMT, int GG>
+template <int FMT, int GG, bool PAIR>
 static const void *decode_fn_gd(int gd) {
-  if (gd == 16) return decode_fn<FMT, GG, 16>();
-  if (gd == 32) return decode_fn<FMT, GG, 32>();
-  return decode_fn<FMT, GG, 64>();
+  if (gd == 16) return decode_fn<FMT, GG, 16, PAIR>();
+  if (gd == 32) return decode_fn<FMT, GG, 32, PAIR>();
+  return decode_fn<FMT, GG, 64, PAIR>();
 }
 
+// Paired workgroups serve gate/up rows cut into two slices of at most 32
+// chunks (GG 16 or 32); single-wave workgroups serve everything else.
 template <int FMT>
-static const void *decode_fn_fmt(int gg, int gd) {
-  if (gg == 16) return decode_fn_gd<FMT, 16>(gd);
-  if (gg == 32) return decode_fn_gd<FMT, 32>(gd);
-  return decode_fn_gd<FMT, 64>(gd);
+static const void *decode_fn_fmt(int gg, int gd, bool pair) {
+  if (pair) return gg == 16 ? decode_fn_gd<FMT, 16, true>(gd) : decode_fn_gd<FMT, 32, true>(gd);
+  if (gg == 16) return decode_fn_gd<FMT, 16, false>(gd);
+  if (gg == 32) return decode_fn_gd<FMT, 32, false>(gd);
+  return decode_fn_gd<FMT, 64, false>(gd);
 }
 
-const void *decode_kernel_fn(int fmt, int gg, int gd) {
-  return fmt == FMT_Q4_0 ? decode_fn_fmt<FMT_Q4_0>(gg, gd) : decode_fn_fmt<FMT_Q8_0>(gg, gd);
+const void *decode_kernel_fn(int fmt, int gg, int gd, bool pair) {
+  return fmt == FMT_Q4_0 ? decode_fn_fmt<FMT_Q4_0>(gg, gd, pair) : decode_fn_fmt<FMT_Q8_0>(gg, gd, pair);
 }
 
-hipError_t launch_decode(const void *fn, uint32_t grid, const DecodeParams &p, hipStream_t st) {
+hipError_t launch_decode(const void *fn, uint32_t grid, uint32_t waves_per_group, const DecodeParams &p,
+                         hipStream_t st) {
   void *args[] = {const_cast<DecodeParams *>(&p)};
-  return hipLaunchKernel(fn, dim3(grid), dim3(64), args, 0, st);
+  return hipLaunchKernel(fn, dim3(grid), dim3(64 * waves_per_group), args, 0, st);
 }
 
 }  // namespace mer

@@ -213,8 +213,9 @@ struct RouterParams {
 
 hipError_t launch_router(const RouterParams &p, hipStream_t st);
 
-const void *decode_kernel_fn(int fmt, int gg, int gd);
-hipError_t launch_decode(const void *fn, uint32_t grid, const DecodeParams &p, hipStream_t st);
+const void *decode_kernel_fn(int fmt, int gg, int gd, bool pair);
+hipError_t launch_decode(const void *fn, uint32_t grid, uint32_t waves_per_group, const DecodeParams &p,
+                         hipStream_t st);
 uint32_t *device_status_ptr();
 hipError_t launch_decode_scratch_prep(uint32_t *ctl, uint32_t n_ctl, uint32_t *zero, size_t n_zero,
                                       uint64_t *epoch_word, hipStream_t st);
