@@ -77,9 +77,8 @@ def test_concurrent_moe_forward_on_four_streams(mer, oracle, gpu, dtype, dm, dff
     for i, (ids, w, x) in enumerate(inputs):
         assert_ffn_close(serial[i], _oracle_moe(oracle, dtype, blobs, ids, w, x, dm, dff), f"serial worker {i}")
 
-    # worker 0 runs on the stream of the serial calls (the device's first
-    # decode stream, whose launches are plain), the others on new streams
-    # (cooperative launches)
+    # worker 0 runs on the stream of the serial calls, the others on new
+    # streams; the library orders their decode launches on the GPU
     streams = [torch.cuda.current_stream(gpu)] + [torch.cuda.Stream(device=gpu) for _ in range(N_WORKERS - 1)]
     outs = [[torch.full((n_tok, dm), float("nan"), device=gpu) for _ in range(ITERS)] for _ in range(N_WORKERS)]
     torch.cuda.synchronize()
@@ -248,3 +247,44 @@ def test_decode_graph_replay(mer, oracle, gpu):
     mer.take_device_status()
     del g
     mer.stream_release(s)
+
+
+def test_decode_beside_busy_device(mer, oracle, gpu):
+    """Decode launches while ordinary kernels keep the device busy from
+    another stream (large matrix products, as an engine's attention would):
+    the persistent grid shares the CUs with them, gets its remaining
+    workgroups as they finish, and every output matches the serial run.
+    (No kernel of the caller spin-waits here: beside such kernels the
+    library makes no progress guarantee.)"""
+    say("decode beside a busy device")
+    dm, dff, n_layers, n_exp, k = 1024, 2048, 4, 6, 2
+    blobs = [[make_expert(oracle, Q4, dm, dff, 900 + l * n_exp + e) for e in range(n_exp)] for l in range(n_layers)]
+    tables = [_table(b, gpu) for b in blobs]
+    rng = np.random.default_rng(31)
+    ids = [to_dev(np.stack([rng.choice(n_exp, k, replace=False)]).astype(np.int32), gpu) for _ in range(n_layers)]
+    ws = [to_dev(rng.random((1, k)).astype(np.float32), gpu) for _ in range(n_layers)]
+    xs = [to_dev(rng.standard_normal((1, dm)).astype(np.float32), gpu) for _ in range(n_layers)]
+
+    def layers(out):
+        return [dict(table=tables[l][1], ids=ids[l], weights=ws[l], x=xs[l], out=out) for l in range(n_layers)]
+
+    ref = torch.zeros((1, dm), device=gpu)
+    mer.moe_forward_layers(mer.WeightDtype.Q4_0, dm, dff, layers(ref))
+    torch.cuda.synchronize()
+    busy = torch.cuda.Stream(device=gpu)
+    mine = torch.cuda.Stream(device=gpu)
+    a = torch.randn((4096, 4096), device=gpu)
+    outs = [torch.zeros((1, dm), device=gpu) for _ in range(8)]
+    with torch.cuda.stream(busy):
+        for _ in range(20):
+            a = torch.tanh(a @ a.T * 1e-3)
+    with torch.cuda.stream(mine):
+        for o in outs:
+            mer.moe_forward_layers(mer.WeightDtype.Q4_0, dm, dff, layers(o))
+    torch.cuda.synchronize()
+    mer.take_device_status()  # raises if a decode wait timed out
+    want = ref.cpu().numpy()
+    for i, o in enumerate(outs):
+        assert np.array_equal(o.cpu().numpy(), want), f"launch {i} beside the busy stream"
+    assert torch.isfinite(a).all()
+    mer.stream_release(mine)
