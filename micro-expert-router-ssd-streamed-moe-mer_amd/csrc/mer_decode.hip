@@ -193,6 +193,16 @@ __device__ __forceinline__ bool arrive_last(uint32_t *ctr, uint32_t expected) {
   return old + 1 == expected;
 }
 
+// Count one arrival without draining this wave's stores first (for counts
+// whose arrivals publish nothing the last arrival reads).
+__device__ __forceinline__ bool arrive_last_nodrain(uint32_t *ctr, uint32_t expected) {
+  uint32_t old = 0;
+  if (lane_id() == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __shfl(old, 0, 64);
+  compiler_fence();
+  return old + 1 == expected;
+}
+
 // Release flag k of (layer, token): its own 256-byte line; holds the epoch
 // of the last launch whose layer was complete for that token.
 __device__ __forceinline__ uint64_t *release_flag(const DecodeParams &p, uint32_t layer, uint32_t t, uint32_t k) {
@@ -777,7 +787,9 @@ __global__ __launch_bounds__(PAIR ? 128 : 64) __attribute__((amdgpu_waves_per_eu
           pack_blocks<FMT, false>(s_h, 1, next_dig, epoch);
         }
         tm.extra = trace_now(p);
-        if (arrive_last(cnt + p.c_c + (size_t)t * kPollStride, p.d_tiles) && lane < kReleaseFan)
+        // the last layer's release flags have no reader
+        if (l + 1 < p.n_layers && arrive_last(cnt + p.c_c + (size_t)t * kPollStride, p.d_tiles) &&
+            lane < kReleaseFan)
           st_dev(release_flag(p, l, t, lane), epoch);
         compiler_fence();
       }
@@ -794,15 +806,19 @@ __global__ __launch_bounds__(PAIR ? 128 : 64) __attribute__((amdgpu_waves_per_eu
   const uint32_t grp = (blockIdx.x * kW + wv) % kExitGroups;
   const uint32_t in_grp = n_waves / kExitGroups + (grp < n_waves % kExitGroups ? 1u : 0u);
   uint32_t *grp_ctr = p.exit_groups + (size_t)grp * kPollStride;
+  // The group arrival drains: this wave's last counter atomics (issued
+  // without waiting for a return) land before the last wave zeroes the
+  // counters.  What the last waves store after that (the group counter's
+  // reset, the zeroed counters, the next epoch) needs no drain: the next
+  // launch on this workspace starts after this kernel has completed.
   if (!arrive_last(grp_ctr, in_grp)) return;
-  if (lane == 0) st_dev(grp_ctr, 0u);  // ready for the next launch (drained by the arrival below)
-  if (arrive_last(p.exit_count, min(n_waves, kExitGroups))) {
+  if (lane == 0) st_dev(grp_ctr, 0u);
+  if (arrive_last_nodrain(p.exit_count, min(n_waves, kExitGroups))) {
     for (uint32_t i = lane; i < p.n_counters; i += 64) st_dev(p.counters + i, 0u);
     if (lane == 0) {
       st_dev(p.abort_flag, 0u);
       const uint64_t seq = __hip_atomic_fetch_add(&g_epoch_seq, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       st_dev(p.epoch_word, (uint64_t)((1ull << 63) | (seq + 1)));
-      drain_stores();
       st_dev(p.exit_count, 0u);
     }
   }
