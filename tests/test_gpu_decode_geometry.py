@@ -1,11 +1,14 @@
 """Every instantiation of the persistent decode kernel against the oracle.
 
 The decode kernel is compiled per (weight format, gate/up lane-group width
-GG, down lane-group width GD), 2 x 3 x 3 = 18 variants; the planner picks
-one from the shape (column chunks per slice <= 16, <= 32 or <= 64 lanes),
-the number of routed instances (narrow layers split gate/up rows into two
+GG, down lane-group width GD), 2 x 3 x 3 = 18 one-wave variants, plus the
+paired two-wave variants for gate/up rows cut into two column slices of
+at most 32 chunks (GG 16 or 32), 2 x 2 x 3 = 12 more; the planner picks one
+from the shape (column chunks per slice <= 16, <= 32 or <= 64 lanes), the
+number of routed instances (narrow layers split gate/up rows into two
 column slices) and the down rows' length (32-chunk slices when they
-divide).  Each case below is built to land on one variant; `_plan` mirrors
+divide).  The paired cases also cross the padding of the item list (the
+gate/up items start at an even index of an even-length layer).  Each case below is built to land on one variant; `_plan` mirrors
 the planner's rule so a change of the rule shows up here as a failed
 geometry assertion rather than as silently lost coverage.  Bar:
 assert_ffn_close against the oracle's routed forward and slot-order combine."""
@@ -27,34 +30,43 @@ def _group_width(chunks: int, min_slices: int = 1) -> int:
     return 16 if cps <= 16 else (32 if cps <= 32 else 64)
 
 
-def _plan(dm: int, dff: int, n_tok: int, k: int) -> tuple[int, int]:
-    """(GG, GD) as plan_decode chooses them (mer_abi.hip)."""
+def _plan(dm: int, dff: int, n_tok: int, k: int) -> tuple[int, int, bool]:
+    """(GG, GD, paired) as plan_decode chooses them (mer_abi.hip)."""
     g_chunks, d_chunks = dm // 64, dff // 64
     narrow = n_tok * k * (dff // 32) < 512 and g_chunks >= 32
     d32 = d_chunks > 64 and d_chunks % 32 == 0 and k * (d_chunks // 32) <= 16
-    return _group_width(g_chunks, 2 if narrow else 1), _group_width(d_chunks, d_chunks // 32 if d32 else 1)
+    g_slices = max(-(-g_chunks // 64), 2 if narrow else 1)
+    gg = _group_width(g_chunks, 2 if narrow else 1)
+    return gg, _group_width(d_chunks, d_chunks // 32 if d32 else 1), g_slices == 2 and gg <= 32
 
 
-# (d_model, d_ff, tokens, top_k) -> (GG, GD)
+# (d_model, d_ff, tokens, top_k) -> (GG, GD, paired)
 SHAPES = {
-    (1024, 1024, 2, 2): (16, 16),
-    (1024, 2048, 2, 2): (16, 32),
-    (1024, 4096, 1, 2): (16, 64),
-    (2048, 1024, 8, 2): (32, 16),
-    (2048, 2048, 4, 2): (32, 32),
-    (4096, 4096, 1, 2): (32, 64),   # narrow: two 32-chunk gate/up slices
-    (4096, 1024, 8, 2): (64, 16),
-    (4096, 2048, 4, 2): (64, 32),
-    (4096, 4096, 2, 2): (64, 64),
+    (1024, 1024, 2, 2): (16, 16, False),
+    (1024, 2048, 2, 2): (16, 32, False),
+    (1024, 4096, 1, 2): (16, 64, False),
+    (2048, 1024, 8, 2): (32, 16, False),
+    (2048, 2048, 4, 2): (32, 32, False),
+    (2048, 4096, 4, 2): (32, 64, False),
+    (4096, 1024, 8, 2): (64, 16, False),
+    (4096, 2048, 4, 2): (64, 32, False),
+    (4096, 4096, 2, 2): (64, 64, False),
+    # narrow layers: two gate/up column slices, paired workgroups
+    (2048, 1024, 2, 2): (16, 16, True),
+    (2048, 2048, 1, 2): (16, 32, True),
+    (2048, 4096, 1, 2): (16, 64, True),
+    (4096, 1024, 1, 2): (32, 16, True),
+    (4096, 2048, 3, 1): (32, 32, True),
+    (4096, 4096, 1, 2): (32, 64, True),
 }
 CASES = [(dt, *shape) for dt in (Q4, Q8) for shape in SHAPES]
 
 
 @pytest.mark.parametrize("dtype,dm,dff,n_tok,k", CASES)
 def test_decode_variant_vs_oracle(mer, oracle, gpu, dtype, dm, dff, n_tok, k):
-    gg, gd = SHAPES[(dm, dff, n_tok, k)]
-    assert _plan(dm, dff, n_tok, k) == (gg, gd)
-    say(f"decode variant fmt={dtype} GG={gg} GD={gd}: dm={dm} dff={dff} tokens={n_tok} top_k={k}")
+    gg, gd, paired = SHAPES[(dm, dff, n_tok, k)]
+    assert _plan(dm, dff, n_tok, k) == (gg, gd, paired)
+    say(f"decode variant fmt={dtype} GG={gg} GD={gd} paired={paired}: dm={dm} dff={dff} tokens={n_tok} top_k={k}")
     rng = np.random.default_rng(dm * 7 + dff + 13 * n_tok + dtype)
     n_exp = 3
     blobs = [make_expert(oracle, dtype, dm, dff, 700 + e) for e in range(n_exp)]
@@ -67,5 +79,5 @@ def test_decode_variant_vs_oracle(mer, oracle, gpu, dtype, dm, dff, n_tok, k):
                           to_dev(x, gpu)).cpu().numpy()
     torch.cuda.synchronize()
     mer.take_device_status()
-    assert_ffn_close(got, want, f"decode variant fmt={dtype} GG={gg} GD={gd}")
+    assert_ffn_close(got, want, f"decode variant fmt={dtype} GG={gg} GD={gd} paired={paired}")
     del devs
