@@ -38,7 +38,12 @@ same workload, starting with that last timed step, on the host's cores (up
 to the 16-thread share of a one-GPU job; host fields in the line):
 q4_0_cpu_reference_forward (dequantise + f32 GEMV) for Q4_0,
 forward_q8_0_direct_into's AVX2 kernel for Q8_0.  Configs 1 and 2 also
-report the same steps under MER_MOE_ROUTE_AFTER_PREV (route_after_prev).
+report the same steps under MER_MOE_ROUTE_AFTER_PREV (route_after_prev)
+and as one call per layer (per_layer).  Configs 0 and 1 also report the same
+steps with MER_MOE_QMM (qmm): Q4_0 through Candle's QMatMul arithmetic, the
+reference engine's default Q4_0 arm, checked against the oracle's
+restatement of it under the bar of tests/test_gpu_qmm.py.  `value` and
+`roofline` stay on q4_0_cpu_reference_forward's semantics.
 """
 from __future__ import annotations
 
@@ -299,6 +304,38 @@ def run_cache_pressure(args, cfg, mer, routing, dev, stream):
     return result
 
 
+def qmm_parity(dm, dff, step, blob_of, gpu_rows):
+    """Parity of a QMatMul-mode launch: the oracle's restatement of
+    run_inference_q4_0_qmm (Q8_0-quantised activations, inference.rs:
+    4159-4243) on the same step, worst |gpu - ref| / allowed under the bar
+    of tests/test_gpu_qmm.py (the FFN bar plus the oracle's flip bound).
+    `step` is a list of rows as in cpu_baseline."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import mer_oracle  # noqa: E402  (test infrastructure, used as the checker)
+
+    threads = baseline_threads()
+    rows, bounds, flagged = [], [], 0
+    for row in step:
+        acc = np.zeros(dm, np.float64)
+        bnd = np.zeros(dm, np.float64)
+        for x, keys, wts in row:
+            res = [mer_oracle.q4_0_qmm_forward_bounded(blob_of(k), x, dm, dff, nthreads=threads) for k in keys]
+            acc += mer_oracle.combine_outputs(np.stack([r[0] for r in res]), np.asarray(wts, np.float32)).astype(
+                np.float64)
+            bnd += sum(abs(float(w)) * r[1].astype(np.float64) for w, r in zip(wts, res))
+            flagged += sum(r[2] for r in res)
+        rows.append(acc)
+        bounds.append(bnd)
+    ref = np.stack(rows)
+    got = np.asarray(gpu_rows, np.float64).reshape(ref.shape)
+    bar = 1e-3 * np.abs(ref) + 1e-3 * max(1.0, 1e-3 * float(np.abs(ref).max()))
+    err = np.abs(ref - got)
+    return {"parity_worst_ratio": float((err / (bar + np.stack(bounds))).max()),
+            "rows_beyond_ffn_bar": int((err > bar).sum()), "h_elements_flagged": int(flagged),
+            "parity_bar": "1e-3 |ref| + 1e-3 max(1, 1e-3 max|ref|) + the oracle's flip bound (h elements within "
+                          "1e-3 steps of a Q8_0 rounding midpoint may round either way in another f32 order)"}
+
+
 def router_pass(gates, xs_d, ids, L, E, K, dm, first_step, n_steps):
     """The GPU LinearGate router (mer_hip_route_linear_gate, row a19) on the
     config-2 steps' hidden states, one call per layer (logits kernel + select
@@ -362,6 +399,8 @@ def main() -> int:
     ap.add_argument("--no-route-after-prev-pass", action="store_true",
                     help="skip the second pass of configs 1 and 2 under MER_MOE_ROUTE_AFTER_PREV (for profiler runs "
                          "whose per-kernel averages should cover the timed launches only)")
+    ap.add_argument("--no-qmm-pass", action="store_true",
+                    help="skip the Q4_0 QMatMul-mode pass (MER_MOE_QMM) reported as `qmm` on configs 0 and 1")
     ap.add_argument("--per-layer", action="store_true",
                     help="one mer_hip_moe_forward call per layer instead of one multi-layer launch per token")
     args = ap.parse_args()
@@ -691,6 +730,50 @@ def main() -> int:
             "note": "the same steps as one mer_hip_moe_forward per layer (MER's call pattern), launched back to "
                     "back; avg_launch_us = HIP events around the pass / launches; frac counts the whole step by "
                     "the host clock, kernel_frac the average launch"}
+    if dtype == Q4 and args.config in (0, 1) and not args.per_layer and not args.route_after_prev \
+            and not args.no_qmm_pass:
+        # The same steps with Candle's QMatMul arithmetic (MER_MOE_QMM): the
+        # engine's default Q4_0 arm (use_qmm_for_q4, engine.rs:1144, :1825),
+        # activations quantised to Q8_0 per block as QMatMul does.
+        if args.config == 0:
+            q_fn = lib.mer_hip_expert_forward_qmm
+            q_args = [a[1:] for a in all_args]
+        else:
+            q_fn = fn
+            q_args = [a[:7] + (a[7] | 16,) + a[8:] for a in all_args]
+        outs.zero_()
+        for s in range(args.warmup):
+            q_fn(*q_args[s])
+        torch.cuda.synchronize()
+        q0 = time.perf_counter()
+        ev_a.record()
+        for s in range(args.warmup, total_steps):
+            rc = q_fn(*q_args[s])
+            if rc:
+                mer.errors.raise_for_status(rc)
+        ev_b.record()
+        torch.cuda.synchronize()
+        q1 = time.perf_counter()
+        mer.take_device_status()
+        q_us = ev_a.elapsed_time(ev_b) * 1e3 / args.steps
+        result["qmm"] = {
+            "value": args.steps / (q1 - q0) * cfg.get("tokens", 1), "unit": cfg["unit"],
+            "ms_per_step": (q1 - q0) * 1e3 / args.steps, "avg_launch_us": q_us,
+            "frac": launch_bytes / (q_us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+            "dtype": "q4_0 weights x Q8_0 activations (Candle QMatMul), int32 block dots, f32 accumulate",
+            "note": "the same steps with MER_MOE_QMM: Q4_0 through Candle's QMatMul arithmetic, the reference "
+                    "engine's default Q4_0 arm; avg_launch_us = HIP events around the pass / launches"}
+        if not args.no_cpu_baseline:
+            q_last = outs[total_steps - 1].cpu().numpy().copy()
+            q_blobs = {}
+
+            def q_blob(e):
+                if e not in q_blobs:
+                    q_blobs[e] = weights[e * ebytes:(e + 1) * ebytes].cpu().numpy()
+                return q_blobs[e]
+
+            result["qmm"].update(qmm_parity(dm, dff, step_rows(total_steps - 1), q_blob, q_last))
+            q_blobs.clear()
     if args.config == 2:
         result["router"] = router_pass(gates, xs_d, ids, L, E, K, dm, args.warmup, min(5, args.steps))
     traffic = read_traffic(args.config) if dominant == "decode" and not args.per_layer else None

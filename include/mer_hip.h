@@ -208,6 +208,14 @@ int mer_hip_expert_forward(int dtype, const void *d_bytes, size_t len,
                            const float *d_x, size_t x_len, size_t d_model,
                            size_t d_ff, float *d_y, size_t y_len, void *stream);
 
+/* dispatch_expert_forward's Q4_0 arm with use_qmm (engine.rs:1825-1830):
+ * run_inference_q4_0_qmm / forward_q4_0_qmm_from_exact_bytes
+ * (inference.rs:4159-4243) on VRAM-resident Q4_0 bytes, with the arithmetic
+ * of MER_MOE_QMM.  Same validation and errors as mer_hip_expert_forward
+ * plus MER_ERR_INVALID_LAYOUT for dims that are not multiples of 64. */
+int mer_hip_expert_forward_qmm(const void *d_bytes, size_t len, const float *d_x, size_t x_len, size_t d_model,
+                               size_t d_ff, float *d_y, size_t y_len, void *stream);
+
 /* Same with host buffers (copies in, runs, copies out, synchronises):
  * the literal signature of forward_q8_0_direct_into / the Q4_0 reference
  * over ExpertResident::data() bytes.  PCIe-inclusive. */
@@ -218,6 +226,19 @@ int mer_hip_expert_forward_host(int dtype, const void *bytes, size_t len,
 /* Flags for mer_hip_moe_forward. */
 #define MER_MOE_RESIDUAL 1u   /* out = x + sum_i w_i y_i                */
 #define MER_MOE_ACCUMULATE 2u /* out = out + sum_i w_i y_i              */
+/* Q4_0 experts through Candle's QMatMul arithmetic: the engine's default
+ * Q4_0 arm (use_qmm_for_q4, engine.rs:1144, :1825-1830 ->
+ * run_inference_q4_0_qmm, inference.rs:4159-4243).  Each projection's
+ * input (x, then h) is quantised to Q8_0 per 32-element block (candle-core
+ * 0.10.2 BlockQ8_0::from_float: d = max|v| / 127 rounded to f16, q =
+ * round(v / d) half away from zero) and every block contributes
+ * sum_i (w_i - 8) q_i * d_w * d_x, as BlockQ4_0::vec_dot does; the block
+ * sums are exact and only their f32 sum order differs from Candle's.
+ * Accepted by mer_hip_moe_forward, _noalloc and _layers; Q8_0 experts ignore
+ * it (use_qmm only switches the Q4_0 arm); d_model and d_ff must be
+ * multiples of 64 (MER_ERR_INVALID_LAYOUT otherwise; not multiples of 32 is
+ * the reference's own InvalidLayout, inference.rs:4211-4215). */
+#define MER_MOE_QMM 16u
 
 /* Fused routed experts + top-k weighted combine for n_tokens decode
  * tokens: the WeightedInto loop of moe_step_inner (engine.rs:5548-5639)

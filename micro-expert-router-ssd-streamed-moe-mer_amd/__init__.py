@@ -38,6 +38,7 @@ from .expert import (
     moe_forward_layers,
     moe_grouped,
     q4_0_forward,
+    q4_0_qmm_forward,
     q4_0_matvec,
     routed_expert_gpu_compatibility,
     routed_expert_matmul_batch,

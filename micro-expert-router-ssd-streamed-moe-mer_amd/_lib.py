@@ -120,6 +120,8 @@ SIGNATURES = {
     "mer_hip_q4_0_matvec": (c_int, [c_void, c_size, c_size, c_size, c_size, c_void, c_void, c_void]),
     "mer_hip_expert_forward": (
         c_int, [c_int, c_void, c_size, c_void, c_size, c_size, c_size, c_void, c_size, c_void]),
+    "mer_hip_expert_forward_qmm": (
+        c_int, [c_void, c_size, c_void, c_size, c_size, c_size, c_void, c_size, c_void]),
     "mer_hip_expert_forward_host": (
         c_int, [c_int, c_void, c_size, c_void, c_size, c_size, c_size, c_void, c_size]),
     "mer_hip_moe_forward": (

@@ -97,7 +97,7 @@ struct DeviceState {
   int cus = 256;
   uint32_t *status = nullptr;
   uint64_t clock_khz = 100000;
-  std::atomic<int> occupancy[2][2][3][3] = {};  // resident decode workgroups per CU, by (pair, fmt, GG, GD)
+  std::atomic<int> occupancy[2][2][2][3][3] = {};  // resident decode workgroups per CU, by (Q8 act, pair, fmt, GG, GD)
   // Device-wide order of persistent decode launches (guarded by
   // g_launch_mu).  The decode grid fills the device and hands items out by
   // static stride, so it needs all of its workgroups resident; two such
@@ -380,6 +380,7 @@ struct DecodePlan {
   int fmt;
   SliceGeom gg, gd;
   bool pair;  // two-wave workgroups: a tile's two gate/up slices add up in LDS
+  bool q8act;  // Q4_0 with Candle's Q8_0 activations (MER_MOE_QMM)
   size_t n_xd, n_gp, n_hd, n_pa;  // floats: x digit lines, gate/up slice partials, h digit lines, down partials
   size_t layer_flags, gd_flags;   // 64-bit release flags
   bool gd_fan;
@@ -391,6 +392,7 @@ void plan_decode(DecodePlan &pl, int dtype, size_t dm, size_t dff, uint32_t n_la
   DeviceState &dev = g_dev[g_device.load()];
   const int fmt = fmt_of(dtype);
   pl.fmt = fmt;
+  pl.q8act = fmt == FMT_Q4_0 && (flags & kFlagQ8Act) != 0;
   DecodeParams &p = pl.p;
   p = DecodeParams{};
   p.swiglu_limit = g_swiglu_limit.load();
@@ -511,9 +513,9 @@ void bind_decode(DecodePlan &pl, float *f, uint32_t *counters, uint32_t *ctl, ui
 int launch_planned(DecodePlan &pl, hipStream_t st, const std::function<hipError_t()> &prep = nullptr) {
   DeviceState &dev = g_dev[g_device.load()];
   DecodeParams &p = pl.p;
-  const void *fn = decode_kernel_fn(pl.fmt, pl.gg.G, pl.gd.G, pl.pair);
+  const void *fn = decode_kernel_fn(pl.fmt, pl.gg.G, pl.gd.G, pl.pair, pl.q8act);
   const uint32_t wpg = pl.pair ? 2u : 1u;
-  std::atomic<int> &occ_slot = dev.occupancy[pl.pair][pl.fmt][g_index(pl.gg.G)][g_index(pl.gd.G)];
+  std::atomic<int> &occ_slot = dev.occupancy[pl.q8act][pl.pair][pl.fmt][g_index(pl.gg.G)][g_index(pl.gd.G)];
   int occ = occ_slot.load();
   if (occ == 0) {
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 64 * wpg, 0);
@@ -1107,6 +1109,41 @@ int mer_hip_expert_forward(int dtype, const void *d_bytes, size_t len, const flo
                      0u, true);
 }
 
+// MER_MOE_QMM runs on the persistent decode kernel only.  It changes Q4_0
+// experts alone: the engine's use_qmm switches only the Q4_0 arm of
+// dispatch_expert_forward (engine.rs:1825-1830), so Q8_0 ignores it.
+static int check_qmm(int dtype, size_t d_model, size_t d_ff, unsigned flags) {
+  if (!(flags & MER_MOE_QMM) || dtype != MER_DTYPE_Q4_0) return MER_OK;
+  if (d_model % 32 || d_ff % 32)
+    return fail(MER_ERR_INVALID_LAYOUT,
+                "Q4_0 QMatMul requires d_model and d_ff to be multiples of 32, got d_model=%zu, d_ff=%zu", d_model, d_ff);
+  if (!decode_eligible(d_model, d_ff, nullptr))
+    return fail(MER_ERR_INVALID_LAYOUT,
+                "the GPU QMatMul path runs on the decode kernel: d_model and d_ff must be multiples of 64, got %zu, %zu",
+                d_model, d_ff);
+  return MER_OK;
+}
+
+int mer_hip_expert_forward_qmm(const void *d_bytes, size_t len, const float *d_x, size_t x_len, size_t d_model,
+                               size_t d_ff, float *d_y, size_t y_len, void *stream) {
+  int rc = require_init();
+  if (rc) return rc;
+  rc = validate(MER_DTYPE_Q4_0, len, x_len, y_len, d_model, d_ff, 0);
+  if (rc) return rc;
+  if (d_model == 0 || d_ff == 0) return fail(MER_ERR_INVALID_LAYOUT, "expert dimensions must be non-zero");
+  if ((rc = check_qmm(MER_DTYPE_Q4_0, d_model, d_ff, MER_MOE_QMM))) return rc;
+  if (!d_bytes || !d_x || !d_y) return fail(MER_ERR_INVALID_LAYOUT, "null device pointer");
+  if ((uintptr_t)d_bytes % 4)
+    return fail(MER_ERR_MISALIGNED, "the GPU QMatMul path needs 4-byte aligned expert bytes");
+  hipStream_t st = (hipStream_t)stream;
+  std::shared_ptr<Workspace> w = workspace_for(st);
+  if (!w) return require_init();
+  std::lock_guard<std::mutex> wl(w->mu);
+  if (w->released) return released_error();
+  return run_experts(*w, MER_DTYPE_Q4_0, d_model, d_ff, 1, 1, nullptr, 0, nullptr, (const uint8_t *)d_bytes, nullptr,
+                     d_x, d_y, MER_MOE_QMM, true);
+}
+
 int mer_hip_expert_forward_host(int dtype, const void *bytes, size_t len, const float *x, size_t x_len,
                                 size_t d_model, size_t d_ff, float *y, size_t y_len) {
   int rc = require_init();
@@ -1165,8 +1202,10 @@ int mer_hip_moe_forward(int dtype, size_t d_model, size_t d_ff, size_t n_tokens,
   rc = mer_routed_expert_gpu_compatibility(dtype, d_model, d_ff);
   if (rc) return rc;
   if (d_model == 0 || d_ff == 0) return fail(MER_ERR_INVALID_LAYOUT, "expert dimensions must be non-zero");
-  if (flags & ~3u) return fail(MER_ERR_INVALID_LAYOUT, "unknown flags 0x%x (CHAIN applies to mer_hip_moe_forward_layers)", flags);
+  if (flags & ~(3u | MER_MOE_QMM))
+    return fail(MER_ERR_INVALID_LAYOUT, "unknown flags 0x%x (CHAIN applies to mer_hip_moe_forward_layers)", flags);
   if ((flags & 3u) == 3u) return fail(MER_ERR_INVALID_LAYOUT, "RESIDUAL and ACCUMULATE are exclusive");
+  if ((rc = check_qmm(dtype, d_model, d_ff, flags))) return rc;
   if (n_tokens == 0 || top_k == 0) return MER_OK;
   if (n_tokens * top_k > (1u << 16) || table_len > UINT32_MAX)
     return fail(MER_ERR_SHAPE_EXCEEDS_WORKSPACE, "too many expert instances");
@@ -1190,7 +1229,7 @@ int mer_hip_moe_forward_noalloc(int dtype, size_t d_model, size_t d_ff, size_t n
     return fail(MER_ERR_UNSUPPORTED_DTYPE, "unsupported expert dtype %d", dtype);
   rc = mer_routed_expert_gpu_compatibility(dtype, d_model, d_ff);
   if (rc) return rc;
-  if (flags & ~3u) return fail(MER_ERR_INVALID_LAYOUT, "unknown flags 0x%x", flags);
+  if (flags & ~(3u | MER_MOE_QMM)) return fail(MER_ERR_INVALID_LAYOUT, "unknown flags 0x%x", flags);
   if ((flags & 3u) == 3u) return fail(MER_ERR_INVALID_LAYOUT, "RESIDUAL and ACCUMULATE are exclusive");
   if (!decode_eligible(d_model, d_ff, nullptr))
     return fail(MER_ERR_INVALID_LAYOUT,
@@ -1287,7 +1326,8 @@ int mer_hip_moe_forward_layers(int dtype, size_t d_model, size_t d_ff, size_t n_
     return fail(MER_ERR_UNSUPPORTED_DTYPE, "unsupported expert dtype %d", dtype);
   rc = mer_routed_expert_gpu_compatibility(dtype, d_model, d_ff);
   if (rc) return rc;
-  if (flags & ~(MER_MOE_RESIDUAL | MER_MOE_ACCUMULATE | MER_MOE_CHAIN | MER_MOE_ROUTE_AFTER_PREV))
+  if ((rc = check_qmm(dtype, d_model, d_ff, flags))) return rc;
+  if (flags & ~(MER_MOE_RESIDUAL | MER_MOE_ACCUMULATE | MER_MOE_CHAIN | MER_MOE_ROUTE_AFTER_PREV | MER_MOE_QMM))
     return fail(MER_ERR_INVALID_LAYOUT, "unknown flags 0x%x", flags);
   if ((flags & 3u) == 3u) return fail(MER_ERR_INVALID_LAYOUT, "RESIDUAL and ACCUMULATE are exclusive");
   if (n_layers == 0 || n_tokens == 0 || top_k == 0) return MER_OK;

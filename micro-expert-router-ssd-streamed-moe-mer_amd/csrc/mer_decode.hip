@@ -286,7 +286,7 @@ __device__ __forceinline__ float span_sum(float v) {
 // format (dword 24 = scale, dwords 25..26 = launch epoch); one wave, lane =
 // group.  DEV: x is read with device-scope loads (it may have been written
 // by another wave of this launch); otherwise x is in LDS.
-template <int FMT, bool DEV>
+template <int FMT, bool DEV, bool Q8ACT = false>
 __device__ __forceinline__ void pack_blocks(const float *x, uint32_t nblocks, uint32_t *dig, uint64_t epoch) {
   using D = DigitTraits<FMT>;
   const uint32_t g = lane_id();
@@ -317,9 +317,9 @@ __device__ __forceinline__ void pack_blocks(const float *x, uint32_t nblocks, ui
     finite &= __shfl_xor(finite, off, 64);
   }
   if (valid) {
-    const BlockScale bs = make_block_scale(amax, finite != 0);
+    const BlockScale bs = Q8ACT ? make_block_scale_q8(amax) : make_block_scale(amax, finite != 0);
     uint32_t plane[D::kPlanes];
-    pack_group<FMT>(v, bs.inv, plane);
+    pack_group<FMT, Q8ACT>(v, bs.inv, plane);
     uint32_t *line = dig + (size_t)b * kLineDwords;
 #pragma unroll
     for (int k = 0; k < D::kPlanes; ++k) st_dev(line + k * D::kGroups + m, plane[k]);
@@ -347,7 +347,7 @@ __device__ __forceinline__ void pack_blocks(const float *x, uint32_t nblocks, ui
 // writer.
 constexpr uint32_t kNoChunk = 0x80000000u;  // beyond num_records: loads return 0
 
-template <int FMT, int G, int R, int S, int NB>
+template <int FMT, int G, int R, int S, int NB, bool Q8ACT>
 struct TileWalk {
   using T = FmtTraits<FMT>;
   static constexpr int kGroups = 64 / G;
@@ -427,7 +427,7 @@ struct TileWalk {
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
-      for (int j = 0; j < R; ++j) v[s * R + j] = chunk_idot<FMT>(wb[s][j], xd, xsc);
+      for (int j = 0; j < R; ++j) v[s * R + j] = chunk_idot<FMT, Q8ACT>(wb[s][j], xd, xsc);
     emit(writer, my_row + pass * kStep, my_s, reduce(v));
   }
 
@@ -516,7 +516,7 @@ __device__ __forceinline__ void fetch_digits(const uint32_t *dig, size_t block0,
 // experts): the slices of a tile are consecutive items, so they meet in one
 // workgroup and their partial sums are added in LDS instead of going
 // through memory and an arrival count (one round trip instead of three).
-template <int FMT, int GG, int GD, bool PAIR>
+template <int FMT, int GG, int GD, bool PAIR, bool Q8ACT>
 __global__ __launch_bounds__(PAIR ? 128 : 64) __attribute__((amdgpu_waves_per_eu(FMT == FMT_Q4_0 ? 3 : 2))) void decode_kernel(DecodeParams p) {
   constexpr uint32_t kW = PAIR ? 2 : 1;  // waves per workgroup
   const uint32_t wv = PAIR ? (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / 64) : 0u;
@@ -607,7 +607,7 @@ __global__ __launch_bounds__(PAIR ? 128 : 64) __attribute__((amdgpu_waves_per_eu
         const uint32_t b0 = part * kPackBlocks;
         const uint32_t nb = min(kPackBlocks, p.xblocks - b0);
         const size_t tb = (size_t)t * p.xblocks + b0;
-        pack_blocks<FMT, true>(xsrc + (size_t)t * p.d_model + (size_t)b0 * 32, nb, xq_dig + tb * kLineDwords, epoch);
+        pack_blocks<FMT, true, Q8ACT>(xsrc + (size_t)t * p.d_model + (size_t)b0 * 32, nb, xq_dig + tb * kLineDwords, epoch);
         signal(cnt + p.c_p + (size_t)t * kPollStride);
       }
     } else if (j < p.off_d) {
@@ -621,7 +621,7 @@ __global__ __launch_bounds__(PAIR ? 128 : 64) __attribute__((amdgpu_waves_per_eu
       if (route_after_prev) wait_input_packed(t);
       const uint8_t *expert = resolve_expert(p, la, inst);
       const uint32_t dslice = tile * 32 / (p.d_cps * 64);
-      using W = TileWalk<FMT, GG, 2, 2, kBuffers>;
+      using W = TileWalk<FMT, GG, 2, 2, kBuffers, Q8ACT>;
       const uint32_t grp = lane / GG, gl = lane % GG;
       const uint32_t c_begin = gs * p.g_cps;
       const uint32_t c = c_begin + gl;
@@ -680,7 +680,7 @@ __global__ __launch_bounds__(PAIR ? 128 : 64) __attribute__((amdgpu_waves_per_eu
       if (pack) {
         wave_lds_sync();
         const size_t hb = (size_t)inst * p.hblocks + tile;
-        pack_blocks<FMT, false>(s_h, 1, hq_dig + hb * kLineDwords, epoch);
+        pack_blocks<FMT, false, Q8ACT>(s_h, 1, hq_dig + hb * kLineDwords, epoch);
         uint32_t *gd = cnt + p.c_gd + ((size_t)inst * p.d_slices + dslice) * kPollStride;
         if (p.gd_release) {
           // the last h tile of the slice releases its D items
@@ -703,7 +703,7 @@ __global__ __launch_bounds__(PAIR ? 128 : 64) __attribute__((amdgpu_waves_per_eu
       const uint32_t inst = t * p.top_k + slot;
       if (route_after_prev) wait_input_packed(t);
       const uint8_t *expert = resolve_expert(p, la, inst);
-      using W = TileWalk<FMT, GD, (GD == 16 ? 2 : 4), 1, kBuffers>;
+      using W = TileWalk<FMT, GD, (GD == 16 ? 2 : 4), 1, kBuffers, Q8ACT>;
       const uint32_t grp = lane / GD, gl = lane % GD;
       const uint32_t c = ds * p.d_cps + gl;
       const bool valid = expert && gl < p.d_cps && c < p.d_chunks;
@@ -784,7 +784,7 @@ __global__ __launch_bounds__(PAIR ? 128 : 64) __attribute__((amdgpu_waves_per_eu
           // or the caller's next input, into layer l+1's digit lines
           wave_lds_sync();
           uint32_t *next_dig = p.xq_dig + ((size_t)(l + 1) * p.n_tok * p.xblocks + (size_t)t * p.xblocks + tile) * kLineDwords;
-          pack_blocks<FMT, false>(s_h, 1, next_dig, epoch);
+          pack_blocks<FMT, false, Q8ACT>(s_h, 1, next_dig, epoch);
         }
         tm.extra = trace_now(p);
         // the last layer's release flags have no reader
@@ -848,30 +848,32 @@ hipError_t launch_decode_scratch_prep(uint32_t *ctl, uint32_t n_ctl, uint32_t *z
   return hipGetLastError();
 }
 
-template <int FMT, int GG, int GD, bool PAIR>
+template <int FMT, int GG, int GD, bool PAIR, bool Q8ACT>
 static const void *decode_fn() {
-  return reinterpret_cast<const void *>(&decode_kernel<FMT, GG, GD, PAIR>);
+  return reinterpret_cast<const void *>(&decode_kernel<FMT, GG, GD, PAIR, Q8ACT>);
 }
 
-template <int FMT, int GG, bool PAIR>
+template <int FMT, int GG, bool PAIR, bool Q8ACT>
 static const void *decode_fn_gd(int gd) {
-  if (gd == 16) return decode_fn<FMT, GG, 16, PAIR>();
-  if (gd == 32) return decode_fn<FMT, GG, 32, PAIR>();
-  return decode_fn<FMT, GG, 64, PAIR>();
+  if (gd == 16) return decode_fn<FMT, GG, 16, PAIR, Q8ACT>();
+  if (gd == 32) return decode_fn<FMT, GG, 32, PAIR, Q8ACT>();
+  return decode_fn<FMT, GG, 64, PAIR, Q8ACT>();
 }
 
 // Paired workgroups serve gate/up rows cut into two slices of at most 32
 // chunks (GG 16 or 32); single-wave workgroups serve everything else.
-template <int FMT>
+template <int FMT, bool Q8ACT>
 static const void *decode_fn_fmt(int gg, int gd, bool pair) {
-  if (pair) return gg == 16 ? decode_fn_gd<FMT, 16, true>(gd) : decode_fn_gd<FMT, 32, true>(gd);
-  if (gg == 16) return decode_fn_gd<FMT, 16, false>(gd);
-  if (gg == 32) return decode_fn_gd<FMT, 32, false>(gd);
-  return decode_fn_gd<FMT, 64, false>(gd);
+  if (pair) return gg == 16 ? decode_fn_gd<FMT, 16, true, Q8ACT>(gd) : decode_fn_gd<FMT, 32, true, Q8ACT>(gd);
+  if (gg == 16) return decode_fn_gd<FMT, 16, false, Q8ACT>(gd);
+  if (gg == 32) return decode_fn_gd<FMT, 32, false, Q8ACT>(gd);
+  return decode_fn_gd<FMT, 64, false, Q8ACT>(gd);
 }
 
-const void *decode_kernel_fn(int fmt, int gg, int gd, bool pair) {
-  return fmt == FMT_Q4_0 ? decode_fn_fmt<FMT_Q4_0>(gg, gd, pair) : decode_fn_fmt<FMT_Q8_0>(gg, gd, pair);
+// q8act: Candle's Q8_0 activations (QMatMul), Q4_0 weights only.
+const void *decode_kernel_fn(int fmt, int gg, int gd, bool pair, bool q8act) {
+  if (fmt != FMT_Q4_0) return decode_fn_fmt<FMT_Q8_0, false>(gg, gd, pair);
+  return q8act ? decode_fn_fmt<FMT_Q4_0, true>(gg, gd, pair) : decode_fn_fmt<FMT_Q4_0, false>(gg, gd, pair);
 }
 
 hipError_t launch_decode(const void *fn, uint32_t grid, uint32_t waves_per_group, const DecodeParams &p,

@@ -166,6 +166,26 @@ __device__ __forceinline__ int32_t quantize_elem(float v, float inv) {
   return (int32_t)q;
 }
 
+// Candle's Q8_0 activation (candle-core 0.10.2 BlockQ8_0::from_float, the
+// input side of QMatMul, run_inference_q4_0_qmm, inference.rs:4159-4243):
+// d = amax / 127 (amax ignores NaN), inv = d != 0 ? 1/d : 0,
+// q = (x * inv).round() as i8 (half away from zero, NaN -> 0, saturating),
+// and the block scale is d rounded to f16.  |q| <= 128 needs only digit
+// planes 0-2 of the 22-bit layout below; planes 3-5 are zero.
+__device__ __forceinline__ BlockScale make_block_scale_q8(float amax) {
+  BlockScale b;
+  const float d = amax / 127.0f;
+  b.inv = d != 0.0f ? 1.0f / d : 0.0f;
+  b.s = (float)(_Float16)d;
+  return b;
+}
+
+__device__ __forceinline__ int32_t quantize_elem_q8(float v, float inv) {
+  const float q = __builtin_roundf(v * inv);
+  if (__builtin_isnan(q)) return 0;
+  return (int32_t)__builtin_fminf(__builtin_fmaxf(q, -128.0f), 127.0f);
+}
+
 __device__ __forceinline__ uint32_t byte_of(uint32_t v, int k) { return (v >> (8 * k)) & 0xffu; }
 
 // Element index (within its block) of slot i of group m.
@@ -177,12 +197,14 @@ __device__ __forceinline__ int group_elem(int m, int i) {
 
 // Pack one group (8 elements for Q4_0, 4 for Q8_0, in group slot order)
 // into its digit-plane dwords: plane[k] goes to digit dword k*groups + m.
-template <int FMT>
+// Q8ACT: the values are Candle's Q8_0 activation instead (Q4_0 only).
+template <int FMT, bool Q8ACT = false>
 __device__ __forceinline__ void pack_group(const float *v, float inv, uint32_t *plane) {
   if constexpr (FMT == FMT_Q4_0) {
     uint32_t t[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) t[i] = ((uint32_t)(quantize_elem(v[i], inv) + 0x888888)) ^ 0x888888u;
+    for (int i = 0; i < 8; ++i)
+      t[i] = ((uint32_t)((Q8ACT ? quantize_elem_q8(v[i], inv) : quantize_elem(v[i], inv)) + 0x888888)) ^ 0x888888u;
     uint32_t E[4], O[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -208,9 +230,23 @@ __device__ __forceinline__ void pack_group(const float *v, float inv, uint32_t *
 // One block's integer dot, recombined to f32: sum_j w_int_j * x_int_j
 // with w_int = q-8 (Q4_0) or q (Q8_0).  `q` holds the block's weight dwords
 // (4 qs dwords for Q4_0, 8 int8 dwords for Q8_0), `dig` its 24 digit dwords.
-template <int FMT>
+// Q8ACT (Q4_0 only): the digits hold a Q8_0 activation in planes 0-2, and
+// the block's dot is that one chain, exact in int32.
+template <int FMT, bool Q8ACT = false>
 __device__ __forceinline__ float block_idot(const uint32_t *q, const uint32_t *dig) {
-  if constexpr (FMT == FMT_Q4_0) {
+  if constexpr (FMT == FMT_Q4_0 && Q8ACT) {
+    uint32_t qs[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) qs[m] = q[m] ^ 0x88888888u;
+    int lo = 0;
+#pragma unroll
+    for (int k = 2; k >= 0; --k) {
+      if (k < 2) lo <<= 4;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) lo = __builtin_amdgcn_sdot8((int)qs[m], (int)dig[k * 4 + m], lo, false);
+    }
+    return (float)lo;
+  } else if constexpr (FMT == FMT_Q4_0) {
     // Horner over the base-16 planes inside the dot chains: each plane's
     // dots accumulate onto the running sum shifted by 4, so a block needs
     // two zeroed accumulators instead of six.  |plane sum| <= 2048, so
@@ -248,15 +284,15 @@ __device__ __forceinline__ float block_idot(const uint32_t *q, const uint32_t *d
 
 // Dot of one 64-weight chunk (two blocks) with its input digits.
 // dig: 48 dwords (block 0 then block 1), sc: the two block scales.
-template <int FMT>
+template <int FMT, bool Q8ACT = false>
 __device__ __forceinline__ float chunk_idot(const uint32_t (&w)[FmtTraits<FMT>::kChunkDwords], const uint32_t *dig,
                                             const float *sc) {
   if constexpr (FMT == FMT_Q4_0) {
     const uint32_t q0[4] = {realign16(w[0], w[1]), realign16(w[1], w[2]), realign16(w[2], w[3]),
                             realign16(w[3], w[4])};
     const uint32_t q1[4] = {w[5], w[6], w[7], w[8]};
-    const float v0 = block_idot<FMT>(q0, dig);
-    const float v1 = block_idot<FMT>(q1, dig + kBlockDigitDwords);
+    const float v0 = block_idot<FMT, Q8ACT>(q0, dig);
+    const float v1 = block_idot<FMT, Q8ACT>(q1, dig + kBlockDigitDwords);
     const float d0 = f16_bits_to_f32(w[0] & 0xffffu) * sc[0];
     const float d1 = f16_bits_to_f32(w[4] >> 16) * sc[1];
     return __builtin_fmaf(d1, v1, d0 * v0);

@@ -87,6 +87,7 @@ constexpr uint32_t kFlagResidual = 1u;    // out = x + sum_i w_i y_i
 constexpr uint32_t kFlagAccumulate = 2u;  // out += sum_i w_i y_i
 constexpr uint32_t kFlagChain = 4u;       // layer l > 0 reads layer l-1's out
 constexpr uint32_t kFlagRouteAfterPrev = 8u;  // layer l > 0 touches its experts after layer l-1 completes
+constexpr uint32_t kFlagQ8Act = 16u;  // Q4_0: activations quantised to Q8_0 as Candle's QMatMul does
 constexpr uint32_t kMaxLayers = 64;
 constexpr uint32_t kLineDwords = 32;     // decode digit block: 24 digit dwords, scale, padding
 constexpr uint32_t kPollStride = 64;     // words between polled decode counters (one 256-byte line each)
@@ -213,7 +214,7 @@ struct RouterParams {
 
 hipError_t launch_router(const RouterParams &p, hipStream_t st);
 
-const void *decode_kernel_fn(int fmt, int gg, int gd, bool pair);
+const void *decode_kernel_fn(int fmt, int gg, int gd, bool pair, bool q8act);
 hipError_t launch_decode(const void *fn, uint32_t grid, uint32_t waves_per_group, const DecodeParams &p,
                          hipStream_t st);
 uint32_t *device_status_ptr();

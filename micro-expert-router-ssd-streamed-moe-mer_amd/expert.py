@@ -35,6 +35,7 @@ MOE_RESIDUAL = 1
 MOE_ACCUMULATE = 2
 MOE_CHAIN = 4
 MOE_ROUTE_AFTER_PREV = 8
+MOE_QMM = 16  # Q4_0 through Candle QMatMul arithmetic (Q8_0 activations)
 
 
 def _device_index(t: torch.Tensor) -> int:
@@ -140,14 +141,34 @@ def q4_0_matvec(weights: torch.Tensor, w_block_off: int, rows: int, columns: int
 
 
 def dispatch_expert_forward(dtype: WeightDtype, resident: torch.Tensor, x: torch.Tensor, d_model: int,
-                            d_ff: int, out: torch.Tensor | None = None) -> torch.Tensor:
+                            d_ff: int, out: torch.Tensor | None = None, use_qmm: bool = False) -> torch.Tensor:
     """dispatch_expert_forward's Q4_0 / Q8_0 arms (engine.rs:1761-1848) on
-    VRAM-resident expert bytes: y = W_down (silu(W_gate x) * (W_up x))."""
+    VRAM-resident expert bytes: y = W_down (silu(W_gate x) * (W_up x)).
+
+    use_qmm: as the engine's flag, Q4_0 runs Candle's QMatMul arithmetic
+    (run_inference_q4_0_qmm, Q8_0-quantised activations) when both dims are
+    multiples of 32, and the dequant reference otherwise (engine.rs:1825-1830);
+    Q8_0 ignores it."""
     _init_for(resident)
     if out is None:
         out = torch.empty(d_model, dtype=torch.float32, device=resident.device)
+    if use_qmm and dtype == WeightDtype.Q4_0 and d_model % 32 == 0 and d_ff % 32 == 0:
+        _call("mer_hip_expert_forward_qmm", _ptr(resident, torch.uint8), resident.numel(), _ptr(x, torch.float32),
+              x.numel(), d_model, d_ff, _ptr(out, torch.float32), out.numel(), _stream())
+        return out
     _call("mer_hip_expert_forward", int(dtype), _ptr(resident, torch.uint8), resident.numel(),
           _ptr(x, torch.float32), x.numel(), d_model, d_ff, _ptr(out, torch.float32), out.numel(), _stream())
+    return out
+
+
+def q4_0_qmm_forward(resident: torch.Tensor, x: torch.Tensor, d_model: int, d_ff: int,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """The device twin of run_inference_q4_0_qmm (inference.rs:4159-4243)."""
+    _init_for(resident)
+    if out is None:
+        out = torch.empty(d_model, dtype=torch.float32, device=resident.device)
+    _call("mer_hip_expert_forward_qmm", _ptr(resident, torch.uint8), resident.numel(), _ptr(x, torch.float32),
+          x.numel(), d_model, d_ff, _ptr(out, torch.float32), out.numel(), _stream())
     return out
 
 
@@ -181,9 +202,10 @@ def expert_forward_host(dtype: WeightDtype, resident: bytes | bytearray | memory
 
 def moe_forward(dtype: WeightDtype, d_model: int, d_ff: int, table: torch.Tensor, expert_ids: torch.Tensor,
                 weights: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = None, *,
-                residual: bool = False, accumulate: bool = False) -> torch.Tensor:
+                residual: bool = False, accumulate: bool = False, qmm: bool = False) -> torch.Tensor:
     """Routed experts + top-k weighted combine for a decode batch: the
-    WeightedInto loop of moe_step_inner (engine.rs:5548-5639).
+    WeightedInto loop of moe_step_inner (engine.rs:5548-5639).  qmm: Q4_0
+    experts with Candle's QMatMul arithmetic (MER_MOE_QMM).
 
     table      int64 [E] device pointers of resident expert blobs (0 = absent),
                or a SlotCache (its device slot table)
@@ -197,7 +219,7 @@ def moe_forward(dtype: WeightDtype, d_model: int, d_ff: int, table: torch.Tensor
         raise ValueError("shape mismatch between expert_ids, weights and x")
     if out is None:
         out = torch.empty_like(x)
-    flags = (MOE_RESIDUAL if residual else 0) | (MOE_ACCUMULATE if accumulate else 0)
+    flags = (MOE_RESIDUAL if residual else 0) | (MOE_ACCUMULATE if accumulate else 0) | (MOE_QMM if qmm else 0)
     _call("mer_hip_moe_forward", int(dtype), d_model, d_ff, n_tokens, top_k, *_table(table),
           _ptr(expert_ids, torch.int32), _ptr(weights, torch.float32), _ptr(x, torch.float32),
           _ptr(out, torch.float32), flags, _stream())
@@ -254,7 +276,8 @@ def moe_grouped(dtype: WeightDtype, d_model: int, d_ff: int, table: torch.Tensor
 
 
 def moe_forward_layers(dtype: WeightDtype, d_model: int, d_ff: int, layers, *, residual: bool = False,
-                       accumulate: bool = False, chain: bool = False, route_after_prev: bool = False) -> None:
+                       accumulate: bool = False, chain: bool = False, route_after_prev: bool = False,
+                       qmm: bool = False) -> None:
     """All MoE layers of one decode step in a single persistent launch: the
     per-layer WeightedInto step of moe_step_inner (engine.rs:5548-5639) for
     every layer (model.rs:2715-2741), layers in order.
@@ -264,7 +287,8 @@ def moe_forward_layers(dtype: WeightDtype, d_model: int, d_ff: int, layers, *, r
     x (f32 [n_tokens, d_model]; may be None for layers > 0 with chain=True)
     and out (f32 [n_tokens, d_model]).  route_after_prev: layer l > 0 reads
     its routing and streams its experts only after layer l-1's output is
-    complete (as when routing is computed from that output).
+    complete (as when routing is computed from that output).  qmm: Q4_0
+    experts with Candle's QMatMul arithmetic (MER_MOE_QMM).
     """
     if not layers:
         return
@@ -282,7 +306,7 @@ def moe_forward_layers(dtype: WeightDtype, d_model: int, d_ff: int, layers, *, r
                                    _ptr(la["weights"], torch.float32), 0 if x is None else _ptr(x, torch.float32),
                                    _ptr(la["out"], torch.float32))
     flags = ((MOE_RESIDUAL if residual else 0) | (MOE_ACCUMULATE if accumulate else 0) | (MOE_CHAIN if chain else 0)
-             | (MOE_ROUTE_AFTER_PREV if route_after_prev else 0))
+             | (MOE_ROUTE_AFTER_PREV if route_after_prev else 0) | (MOE_QMM if qmm else 0))
     _call("mer_hip_moe_forward_layers", int(dtype), d_model, d_ff, len(layers), n_tokens, top_k, arr, flags, _stream())
 
 

@@ -395,6 +395,159 @@ int mo_q4_0_reference_forward(const uint8_t *bytes, size_t len, const float *x,
   return dequant_forward(MO_DTYPE_Q4_0, bytes, x, d_model, d_ff, y, nthreads);
 }
 
+/* ------------------------------------------------------------------ */
+/* Q4_0 through Candle's QMatMul: run_inference_q4_0_qmm (inference.rs:
+ * 4159-4201) -> forward_q4_0_qmm_from_exact_bytes (:4204-4243) ->
+ * forward_qmm (:4102-4127), the engine's default Q4_0 arm when both dims
+ * are multiples of 32 (use_qmm_for_q4 = true, engine.rs:1144, :1825).
+ * The arithmetic lives in candle-core 0.10.2 (Cargo.lock:340-342; a
+ * crates.io dependency, not vendored).  Its published quantized CPU matmul
+ * converts each activation row to the weight type's vec-dot type, Q8_0 for
+ * Q4_0 (k_quants.rs BlockQ8_0::from_float), per 32-element block:
+ *   amax = max |x| (f32::max, so NaN is ignored), d = amax / 127,
+ *   id = d != 0 ? 1 / d : 0, q = (x * id).round() as i8, d kept as f16;
+ * then BlockQ4_0::vec_dot per output row, over the row's blocks in order:
+ *   sumi = sum_{j<16} ((w_j & 15) - 8) q_j + ((w_j >> 4) - 8) q_{j+16}
+ *   sumf += sumi as f32 * f16(d_w) * f16(d_x).
+ * This is that scalar form; Candle's AVX form sums the same integer block
+ * dots in another f32 order, so bit-level parity with Candle stays unpinned
+ * (the reference pins QMM only to 5e-2 of the dequant path,
+ * inference.rs:6547-6594).  The SwiGLU between the projections is
+ * forward_qmm's: clamp_swiglu_gate, silu, mul; the down projection
+ * quantises h the same way.  pinned by: the reference's own
+ * QMM-vs-dequant test (same generator and tolerance), a float64 brute
+ * force of the quantisation and dot from the closed forms, and
+ * half-way rounding cases (tests/test_oracle_qmm.py).                  */
+void mo_quantize_row_q8_0_candle(const float *x, size_t n, int8_t *q, float *d_out) {
+  for (size_t b = 0; b < n / 32; ++b) {
+    const float *xb = x + b * 32;
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+      float a = fabsf(xb[j]);
+      if (a > amax) amax = a; /* f32::max: a NaN operand yields the other */
+    }
+    float d = amax / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    for (int j = 0; j < 32; ++j) {
+      int32_t v = mo_round_to_i32(xb[j] * id);
+      q[b * 32 + j] = (int8_t)(v > 127 ? 127 : (v < -128 ? -128 : v)); /* `as i8` saturates */
+    }
+    d_out[b] = mo_f16_to_f32(mo_f32_to_f16(d));
+  }
+}
+
+struct qmm_ctx {
+  const uint8_t *w; /* Q4_0 rows of `cols` elements */
+  const int8_t *q;  /* Q8_0 activation */
+  const float *dq;  /* its block scales */
+  float *y;
+  size_t cols;
+};
+static void qmm_rows(void *p, size_t b, size_t e) {
+  struct qmm_ctx *c = (struct qmm_ctx *)p;
+  size_t nb = c->cols / 32;
+  for (size_t r = b; r < e; ++r) {
+    const uint8_t *row = c->w + r * nb * Q4_BYTES;
+    float sumf = 0.0f;
+    for (size_t k = 0; k < nb; ++k) {
+      const uint8_t *blk = row + k * Q4_BYTES;
+      const int8_t *qb = c->q + k * 32;
+      int32_t sumi = 0;
+      for (int j = 0; j < 16; ++j) {
+        int32_t v0 = (int32_t)(blk[2 + j] & 15) - 8, v1 = (int32_t)(blk[2 + j] >> 4) - 8;
+        sumi += v0 * qb[j] + v1 * qb[j + 16];
+      }
+      sumf += (float)sumi * block_scale(blk) * c->dq[k];
+    }
+    c->y[r] = sumf;
+  }
+}
+
+/* Q4_0 weight (r, c) of a row-major projection with `cols` columns. */
+static float q4_weight(const uint8_t *proj, size_t cols, size_t r, size_t c) {
+  const uint8_t *blk = proj + (r * (cols / 32) + c / 32) * Q4_BYTES;
+  unsigned j = (unsigned)(c % 32);
+  int nib = j < 16 ? (blk[2 + j] & 15) : (blk[2 + j - 16] >> 4);
+  return block_scale(blk) * (float)(nib - 8);
+}
+
+/* flip_bound (optional, [d_model]): what the down projection's output may
+ * move by when another implementation forms h in another f32 order.  An h
+ * element whose scaled value h * id lies within `margin` of a rounding
+ * midpoint k + 0.5 may round to the neighbouring Q8_0 step there, which
+ * moves row r by |W_d[r, j]| * d_j; a block whose d = amax / 127 lies
+ * within relative `margin` / 127 of an f16 midpoint may take the
+ * neighbouring f16 scale, which moves row r by the block's
+ * sum_j |W_d[r, j] q_j| times that f16 step.  *n_flagged counts both. */
+int mo_q4_0_qmm_forward_ex(const uint8_t *bytes, size_t len, const float *x, size_t d_model, size_t d_ff, float *y,
+                           float *flip_bound, float margin, size_t *n_flagged, int nthreads) {
+  size_t need;
+  int st = mo_validate_q4_0(len, d_model, d_ff, 0, &need);
+  if (st != MO_OK) return st;
+  if (d_model % 32 != 0 || d_ff % 32 != 0) return MO_ERR_INVALID_LAYOUT; /* :4211-4215 */
+  size_t pb = (d_model * d_ff / 32) * Q4_BYTES;
+  size_t big = d_model > d_ff ? d_model : d_ff;
+  int8_t *q = (int8_t *)malloc(big);
+  float *dq = (float *)malloc(sizeof(float) * (big / 32 + 1));
+  float *g = (float *)malloc(sizeof(float) * d_ff * 2);
+  if (!q || !dq || !g) {
+    free(q);
+    free(dq);
+    free(g);
+    return MO_ERR_COMPUTE;
+  }
+  float *u = g + d_ff;
+  mo_quantize_row_q8_0_candle(x, d_model, q, dq);
+  struct qmm_ctx c1 = {bytes, q, dq, g, d_model}, c2 = {bytes + pb, q, dq, u, d_model};
+  par_row_chunks(d_ff, d_model, nthreads, qmm_rows, &c1);
+  par_row_chunks(d_ff, d_model, nthreads, qmm_rows, &c2);
+  for (size_t i = 0; i < d_ff; ++i) g[i] = mo_silu(clamp_gate(g[i])) * u[i];
+  mo_quantize_row_q8_0_candle(g, d_ff, q, dq);
+  struct qmm_ctx c3 = {bytes + 2 * pb, q, dq, y, d_ff};
+  par_row_chunks(d_model, d_ff, nthreads, qmm_rows, &c3);
+  if (flip_bound) {
+    const uint8_t *wd = bytes + 2 * pb;
+    size_t flagged = 0;
+    for (size_t r = 0; r < d_model; ++r) flip_bound[r] = 0.0f;
+    for (size_t b = 0; b < d_ff / 32; ++b) {
+      const float *hb = g + b * 32;
+      float amax = 0.0f;
+      for (int j = 0; j < 32; ++j) {
+        float a = fabsf(hb[j]);
+        if (a > amax) amax = a;
+      }
+      float d = amax / 127.0f;
+      float id = d != 0.0f ? 1.0f / d : 0.0f;
+      for (int j = 0; j < 32; ++j) {
+        float v = hb[j] * id;
+        if (!(fabsf(fabsf(v - floorf(v)) - 0.5f) < margin)) continue;
+        ++flagged;
+        for (size_t r = 0; r < d_model; ++r) flip_bound[r] += fabsf(q4_weight(wd, d_ff, r, b * 32 + j)) * dq[b];
+      }
+      float lo = mo_f16_to_f32(mo_f32_to_f16(d * (1.0f - margin / 127.0f)));
+      float hi = mo_f16_to_f32(mo_f32_to_f16(d * (1.0f + margin / 127.0f)));
+      if (lo != hi) {
+        ++flagged;
+        for (size_t r = 0; r < d_model; ++r) {
+          float sum = 0.0f;
+          for (int j = 0; j < 32; ++j) sum += fabsf(q4_weight(wd, d_ff, r, b * 32 + j) * (float)q[b * 32 + j]);
+          flip_bound[r] += sum * (hi - lo);
+        }
+      }
+    }
+    if (n_flagged) *n_flagged = flagged;
+  }
+  free(q);
+  free(dq);
+  free(g);
+  return MO_OK;
+}
+
+int mo_q4_0_qmm_forward(const uint8_t *bytes, size_t len, const float *x, size_t d_model, size_t d_ff, float *y,
+                        int nthreads) {
+  return mo_q4_0_qmm_forward_ex(bytes, len, x, d_model, d_ff, y, NULL, 0.0f, NULL, nthreads);
+}
+
 /* inference.rs:1868-1919 from_bytes_q8_0 + ExpertWeights::forward. */
 int mo_q8_0_dequant_forward(const uint8_t *bytes, size_t len, const float *x,
                             size_t d_model, size_t d_ff, float *y,

@@ -55,6 +55,12 @@ int mo_validate_q8_direct(size_t len, size_t x_len, size_t y_len,
                           size_t d_model, size_t d_ff, size_t *need_out);
 
 /* ---- expert forward ----------------------------------------------- */
+/* Candle QMatMul Q4_0 path (activations quantised to Q8_0). */
+void mo_quantize_row_q8_0_candle(const float *x, size_t n, int8_t *q, float *d_out);
+int mo_q4_0_qmm_forward(const uint8_t *bytes, size_t len, const float *x, size_t d_model, size_t d_ff, float *y,
+                        int nthreads);
+int mo_q4_0_qmm_forward_ex(const uint8_t *bytes, size_t len, const float *x, size_t d_model, size_t d_ff, float *y,
+                           float *flip_bound, float margin, size_t *n_flagged, int nthreads);
 int mo_q4_0_reference_forward(const uint8_t *bytes, size_t len, const float *x,
                               size_t d_model, size_t d_ff, float *y,
                               int nthreads);

@@ -36,6 +36,10 @@ _SIG = {
     "mo_validate_q4_0": (ctypes.c_int, [_sz, _sz, _sz, _sz, ctypes.POINTER(_sz)]),
     "mo_validate_q8_direct": (ctypes.c_int, [_sz, _sz, _sz, _sz, _sz, ctypes.POINTER(_sz)]),
     "mo_q4_0_reference_forward": (ctypes.c_int, [_u8p, _sz, _f32p, _sz, _sz, _f32p, ctypes.c_int]),
+    "mo_q4_0_qmm_forward": (ctypes.c_int, [_u8p, _sz, _f32p, _sz, _sz, _f32p, ctypes.c_int]),
+    "mo_q4_0_qmm_forward_ex": (ctypes.c_int, [_u8p, _sz, _f32p, _sz, _sz, _f32p, _f32p, ctypes.c_float,
+                                              ctypes.POINTER(_sz), ctypes.c_int]),
+    "mo_quantize_row_q8_0_candle": (None, [_f32p, _sz, ctypes.POINTER(ctypes.c_int8), _f32p]),
     "mo_q8_0_dequant_forward": (ctypes.c_int, [_u8p, _sz, _f32p, _sz, _sz, _f32p, ctypes.c_int]),
     "mo_q8_0_direct_forward": (
         ctypes.c_int, [_u8p, _sz, _f32p, _sz, _sz, _sz, _f32p, _sz, ctypes.c_int, ctypes.c_int]),
@@ -159,6 +163,49 @@ def q4_0_reference_forward(blob: np.ndarray, x: np.ndarray, d_model: int, d_ff: 
     if rc:
         raise ValueError(f"oracle q4_0 forward status {rc}")
     return y
+
+
+def q4_0_qmm_forward(blob: np.ndarray, x: np.ndarray, d_model: int, d_ff: int,
+                     nthreads: int = 8) -> np.ndarray:
+    """run_inference_q4_0_qmm (inference.rs:4159-4243): Candle QMatMul with
+    Q8_0-quantised activations (mo_q4_0_qmm_forward)."""
+    y = np.zeros(d_model, np.float32)
+    xa = np.ascontiguousarray(x, np.float32)
+    rc = lib().mo_q4_0_qmm_forward(_u8(blob), blob.size, _f(xa), d_model, d_ff, _f(y), nthreads)
+    if rc:
+        raise ValueError(f"oracle q4_0 qmm forward status {rc}")
+    return y
+
+
+# Distance from a Q8_0 rounding midpoint, in quantisation steps, within which
+# two f32 evaluation orders of h may round an element differently (a few
+# times the f32 noise of h measured in steps, ~1e-4).
+QMM_FLIP_MARGIN = 1e-3
+
+
+def q4_0_qmm_forward_bounded(blob: np.ndarray, x: np.ndarray, d_model: int, d_ff: int,
+                             margin: float = QMM_FLIP_MARGIN, nthreads: int = 8):
+    """q4_0_qmm_forward plus its flip bound (mo_q4_0_qmm_forward_ex):
+    returns (y, bound[d_model], n_flagged)."""
+    y = np.zeros(d_model, np.float32)
+    bound = np.zeros(d_model, np.float32)
+    n = _sz(0)
+    xa = np.ascontiguousarray(x, np.float32)
+    rc = lib().mo_q4_0_qmm_forward_ex(_u8(blob), blob.size, _f(xa), d_model, d_ff, _f(y), _f(bound), margin,
+                                      ctypes.byref(n), nthreads)
+    if rc:
+        raise ValueError(f"oracle q4_0 qmm forward status {rc}")
+    return y, bound, n.value
+
+
+def quantize_row_q8_0_candle(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Candle's BlockQ8_0::from_float over a row (len a multiple of 32):
+    int8 values and the f16-rounded block scales as f32."""
+    xa = np.ascontiguousarray(x, np.float32)
+    q = np.zeros(xa.size, np.int8)
+    d = np.zeros(xa.size // 32, np.float32)
+    lib().mo_quantize_row_q8_0_candle(_f(xa), xa.size, q.ctypes.data_as(ctypes.POINTER(ctypes.c_int8)), _f(d))
+    return q, d
 
 
 def q8_0_dequant_forward(blob: np.ndarray, x: np.ndarray, d_model: int, d_ff: int,
