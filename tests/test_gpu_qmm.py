@@ -159,3 +159,22 @@ def test_qmm_layout_errors(mer, oracle, gpu):
     got = mer.dispatch_expert_forward(mer.WeightDtype.Q4_0, to_dev(blob, gpu), to_dev(x, gpu), dm, dff,
                                       use_qmm=True).cpu().numpy()
     assert_ffn_close(got, oracle.q4_0_reference_forward(blob, x, dm, dff), "qmm fallback")
+
+
+def test_qmm_non_finite_inputs_follow_the_oracle(mer, oracle, gpu):
+    """Candle's quantisation ignores a NaN in the block maximum and turns the
+    NaN element into 0; an infinite element makes the block scale infinite,
+    so the outputs become NaN.  The GPU mode agrees on which outputs are NaN
+    and on the finite ones."""
+    dm, dff = 128, 256
+    blob = make_expert(oracle, Q4, dm, dff, 5)
+    for label, bad in (("nan", np.nan), ("inf", np.inf)):
+        say(f"qmm non-finite input {label}")
+        x = np.random.default_rng(3).standard_normal(dm).astype(np.float32)
+        x[37] = bad
+        want, bound, _ = oracle.q4_0_qmm_forward_bounded(blob, x, dm, dff)
+        got = mer.q4_0_qmm_forward(to_dev(blob, gpu), to_dev(x, gpu), dm, dff).cpu().numpy()
+        assert np.array_equal(np.isnan(got), np.isnan(want)), label
+        ok = ~np.isnan(want)
+        if ok.any():
+            assert_qmm_close(got[ok], want[ok], bound[ok], f"qmm {label}")
