@@ -234,9 +234,9 @@ int mer_hip_expert_forward_host(int dtype, const void *bytes, size_t len,
  * round(v / d) half away from zero) and every block contributes
  * sum_i (w_i - 8) q_i * d_w * d_x, as BlockQ4_0::vec_dot does; the block
  * sums are exact and only their f32 sum order differs from Candle's.
- * Accepted by mer_hip_moe_forward, _noalloc and _layers; Q8_0 experts ignore
- * it (use_qmm only switches the Q4_0 arm); d_model and d_ff must be
- * multiples of 64 (MER_ERR_INVALID_LAYOUT otherwise; not multiples of 32 is
+ * Accepted by mer_hip_moe_forward, _noalloc, _layers and _grouped; Q8_0
+ * experts ignore it (use_qmm only switches the Q4_0 arm); d_model and d_ff
+ * must be multiples of 64 (MER_ERR_INVALID_LAYOUT otherwise; not multiples of 32 is
  * the reference's own InvalidLayout, inference.rs:4211-4215). */
 #define MER_MOE_QMM 16u
 

@@ -809,6 +809,7 @@ int run_grouped(Workspace &w, int dtype, size_t dm, size_t dff, uint32_t n_token
   p.x = x;
   p.out = out;
   p.flags = flags;
+  p.q8act = dtype == MER_DTYPE_Q4_0 && (flags & MER_MOE_QMM) ? 1u : 0u;
   p.n_tok = n_tokens;
   p.top_k = top_k;
   p.n_pairs = n_tokens * top_k;
@@ -1109,9 +1110,10 @@ int mer_hip_expert_forward(int dtype, const void *d_bytes, size_t len, const flo
                      0u, true);
 }
 
-// MER_MOE_QMM runs on the persistent decode kernel only.  It changes Q4_0
-// experts alone: the engine's use_qmm switches only the Q4_0 arm of
-// dispatch_expert_forward (engine.rs:1825-1830), so Q8_0 ignores it.
+// MER_MOE_QMM runs on the persistent decode kernel and the grouped path
+// (both need multiples of 64).  It changes Q4_0 experts alone: the engine's
+// use_qmm switches only the Q4_0 arm of dispatch_expert_forward
+// (engine.rs:1825-1830), so Q8_0 ignores it.
 static int check_qmm(int dtype, size_t d_model, size_t d_ff, unsigned flags) {
   if (!(flags & MER_MOE_QMM) || dtype != MER_DTYPE_Q4_0) return MER_OK;
   if (d_model % 32 || d_ff % 32)
@@ -1296,7 +1298,7 @@ int mer_hip_moe_grouped(int dtype, size_t d_model, size_t d_ff, size_t n_tokens,
     return fail(MER_ERR_UNSUPPORTED_DTYPE, "unsupported expert dtype %d", dtype);
   rc = mer_routed_expert_gpu_compatibility(dtype, d_model, d_ff);
   if (rc) return rc;
-  if (flags & ~3u) return fail(MER_ERR_INVALID_LAYOUT, "unknown flags 0x%x", flags);
+  if (flags & ~(3u | MER_MOE_QMM)) return fail(MER_ERR_INVALID_LAYOUT, "unknown flags 0x%x", flags);
   if ((flags & 3u) == 3u) return fail(MER_ERR_INVALID_LAYOUT, "RESIDUAL and ACCUMULATE are exclusive");
   if (d_model == 0 || d_ff == 0 || d_model % 64 || d_ff % 64)
     return fail(MER_ERR_INVALID_LAYOUT, "the grouped path needs d_model and d_ff to be non-zero multiples of 64, got %zu, %zu",

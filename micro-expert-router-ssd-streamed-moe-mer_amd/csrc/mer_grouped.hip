@@ -94,7 +94,10 @@ __device__ __forceinline__ bool pair_valid(const GroupedParams &p, uint32_t pair
 // 32-byte record {v0[8], v1[8], v2[8], f32 block scale, 0}, so a reader
 // gets a k-group's three digit planes and the block's scale with two
 // 16-byte loads.  Only lanes with `store` write.
-__device__ __forceinline__ void quant_group(const float (&v)[8], uint32_t *dst, bool store) {
+// q8: Candle's Q8_0 activation instead (QMatMul, MER_MOE_QMM): scale
+// d = amax / 127 kept as f16, q = round(v / d) half away from zero (NaN ->
+// 0), so |q| <= 128 lands in plane 0 and planes 1-2 are zero.
+__device__ __forceinline__ void quant_group(const float (&v)[8], uint32_t *dst, bool store, bool q8) {
   float amax = 0.f;
   int finite = 1;
 #pragma unroll
@@ -108,7 +111,11 @@ __device__ __forceinline__ void quant_group(const float (&v)[8], uint32_t *dst, 
     finite &= __shfl_xor(finite, off, 64);
   }
   float s, inv;
-  if (!finite) {
+  if (q8) {
+    const float d = amax / 127.0f;
+    inv = d != 0.0f ? 1.0f / d : 0.0f;
+    s = (float)(_Float16)d;
+  } else if (!finite) {
     s = __builtin_nanf("");
     inv = 0.f;
   } else if (amax == 0.f) {
@@ -121,8 +128,14 @@ __device__ __forceinline__ void quant_group(const float (&v)[8], uint32_t *dst, 
   uint32_t d[6] = {0u, 0u, 0u, 0u, 0u, 0u};
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    float q = __builtin_rintf(v[i] * inv);
-    q = __builtin_fminf(__builtin_fmaxf(q, -kGIntMax), kGIntMax);
+    float q;
+    if (q8) {
+      q = __builtin_roundf(v[i] * inv);
+      q = __builtin_isnan(q) ? 0.f : __builtin_fminf(__builtin_fmaxf(q, -128.0f), 127.0f);
+    } else {
+      q = __builtin_rintf(v[i] * inv);
+      q = __builtin_fminf(__builtin_fmaxf(q, -kGIntMax), kGIntMax);
+    }
     const uint32_t u = ((uint32_t)((int32_t)q + 0x808080)) ^ 0x808080u;  // three balanced digits
 #pragma unroll
     for (int k = 0; k < 3; ++k) d[2 * k + (i >> 2)] |= ((u >> (8 * k)) & 0xffu) << (8 * (i & 3));
@@ -151,7 +164,7 @@ __global__ __launch_bounds__(1024) void group_kernel(GroupedParams p) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = 0.f;
     }
-    quant_group(v, p.xg + ((size_t)tb * 4 + m) * kGRec, valid);
+    quant_group(v, p.xg + ((size_t)tb * 4 + m) * kGRec, valid, p.q8act != 0);
     return;
   }
 
@@ -516,7 +529,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kGWavesPerE
       const uint32_t pr = __shfl(pair, (int)c, 64);  // lane c of every wave holds column c's pair
       const bool ok = pr != 0xffffffffu;
       const size_t hb = (size_t)(ok ? pr : 0) * p.hblocks + rt * kOwn + hk;
-      quant_group(h, p.hg + (hb * 4 + m) * kGRec, ok);
+      quant_group(h, p.hg + (hb * 4 + m) * kGRec, ok, p.q8act != 0);
     }
   } else {
     if (col_ok) {

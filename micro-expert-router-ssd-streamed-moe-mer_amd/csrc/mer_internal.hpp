@@ -172,6 +172,7 @@ struct GroupedParams {
   const float *x;            // [n_tok][d_model]
   float *out;                // [n_tok][d_model]
   uint32_t flags;
+  uint32_t q8act;            // Q4_0 under MER_MOE_QMM: inputs quantised as Candle's Q8_0
   uint32_t n_tok, top_k, n_pairs;
   uint32_t d_model, d_ff, xblocks, hblocks;
   float swiglu_limit;        // gate clamp before SiLU (+inf = none)

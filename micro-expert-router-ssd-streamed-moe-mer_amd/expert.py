@@ -257,18 +257,19 @@ def expert_matmul(dtype: WeightDtype, d_model: int, d_ff: int, table: torch.Tens
 
 def moe_grouped(dtype: WeightDtype, d_model: int, d_ff: int, table: torch.Tensor, expert_ids: torch.Tensor,
                 weights: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = None, *,
-                residual: bool = False, accumulate: bool = False) -> torch.Tensor:
+                residual: bool = False, accumulate: bool = False, qmm: bool = False) -> torch.Tensor:
     """moe_forward for a multi-token batch on the grouped int8-MFMA path:
     pairs grouped by expert on the device, each expert's weights read once
     for all of its tokens (the batched routed_expert_matmul_batch_q4,
-    backend/mod.rs:4401-4418).  Same arguments and combine as moe_forward."""
+    backend/mod.rs:4401-4418).  Same arguments and combine as moe_forward;
+    qmm: Q4_0 experts with Candle's QMatMul arithmetic (MER_MOE_QMM)."""
     _init_for(x)
     n_tokens, top_k = expert_ids.shape
     if weights.shape != expert_ids.shape or x.shape != (n_tokens, d_model):
         raise ValueError("shape mismatch between expert_ids, weights and x")
     if out is None:
         out = torch.empty_like(x)
-    flags = (MOE_RESIDUAL if residual else 0) | (MOE_ACCUMULATE if accumulate else 0)
+    flags = (MOE_RESIDUAL if residual else 0) | (MOE_ACCUMULATE if accumulate else 0) | (MOE_QMM if qmm else 0)
     _call("mer_hip_moe_grouped", int(dtype), d_model, d_ff, n_tokens, top_k, *_table(table),
           _ptr(expert_ids, torch.int32), _ptr(weights, torch.float32), _ptr(x, torch.float32),
           _ptr(out, torch.float32), flags, _stream())

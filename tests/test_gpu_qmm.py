@@ -178,3 +178,32 @@ def test_qmm_non_finite_inputs_follow_the_oracle(mer, oracle, gpu):
         ok = ~np.isnan(want)
         if ok.any():
             assert_qmm_close(got[ok], want[ok], bound[ok], f"qmm {label}")
+
+
+def test_grouped_qmm_vs_oracle(mer, oracle, gpu):
+    """The grouped int8-MFMA path under MER_MOE_QMM: Candle's Q8_0 value sits
+    in the first of its three digit planes, so the contraction is the same
+    and only the input quantisation changes."""
+    dm, dff, n_exp, n_tok, k = 512, 1024, 6, 24, 2
+    say(f"qmm grouped dm={dm} dff={dff} tokens={n_tok}")
+    blobs = [make_expert(oracle, Q4, dm, dff, 20 + e) for e in range(n_exp)]
+    devs, table = _table(blobs, gpu)
+    rng = np.random.default_rng(21)
+    ids = np.stack([rng.choice(n_exp, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    w = rng.random((n_tok, k)).astype(np.float32)
+    x = rng.standard_normal((n_tok, dm)).astype(np.float32)
+    want = np.zeros((n_tok, dm), np.float32)
+    bound = np.zeros((n_tok, dm), np.float64)
+    deq = np.zeros((n_tok, dm), np.float32)
+    for t in range(n_tok):
+        res = [oracle.q4_0_qmm_forward_bounded(blobs[i], x[t], dm, dff) for i in ids[t]]
+        want[t] = oracle.combine_outputs(np.stack([r[0] for r in res]), w[t])
+        bound[t] = sum(float(w[t, i]) * res[i][1].astype(np.float64) for i in range(k))
+        deq[t] = oracle.combine_outputs(
+            np.stack([oracle.q4_0_reference_forward(blobs[i], x[t], dm, dff) for i in ids[t]]), w[t])
+    got = mer.moe_grouped(mer.WeightDtype.Q4_0, dm, dff, table, to_dev(ids, gpu), to_dev(w, gpu), to_dev(x, gpu),
+                          qmm=True).cpu().numpy()
+    assert_qmm_close(got, want, bound, "qmm grouped")
+    _closer_to_qmm(got, want, deq, "qmm grouped")
+    mer.take_device_status()
+    del devs
