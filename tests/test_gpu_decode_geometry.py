@@ -11,7 +11,8 @@ divide).  The paired cases also cross the padding of the item list (the
 gate/up items start at an even index of an even-length layer).  Each case below is built to land on one variant; `_plan` mirrors
 the planner's rule so a change of the rule shows up here as a failed
 geometry assertion rather than as silently lost coverage.  Bar:
-assert_ffn_close against the oracle's routed forward and slot-order combine."""
+assert_ffn_close against the oracle's routed forward and slot-order combine.  The
+Q4_0 instances of the QMatMul mode (15 more) run the same shapes."""
 from __future__ import annotations
 
 import numpy as np
@@ -80,4 +81,35 @@ def test_decode_variant_vs_oracle(mer, oracle, gpu, dtype, dm, dff, n_tok, k):
     torch.cuda.synchronize()
     mer.take_device_status()
     assert_ffn_close(got, want, f"decode variant fmt={dtype} GG={gg} GD={gd} paired={paired}")
+    del devs
+
+
+@pytest.mark.parametrize("dm,dff,n_tok,k", list(SHAPES))
+def test_decode_qmm_variant_vs_oracle(mer, oracle, gpu, dm, dff, n_tok, k):
+    """The 15 Q4_0 instances of the QMatMul mode (MER_MOE_QMM, Candle's
+    Q8_0 activations), one per shape above, against the oracle's restatement
+    of run_inference_q4_0_qmm under the bar of test_gpu_qmm (the FFN bar plus
+    the oracle's flip bound)."""
+    from test_gpu_qmm import assert_qmm_close
+
+    gg, gd, paired = SHAPES[(dm, dff, n_tok, k)]
+    say(f"decode qmm variant GG={gg} GD={gd} paired={paired}: dm={dm} dff={dff} tokens={n_tok} top_k={k}")
+    rng = np.random.default_rng(dm * 5 + dff + 11 * n_tok)
+    n_exp = 3
+    blobs = [make_expert(oracle, Q4, dm, dff, 800 + e) for e in range(n_exp)]
+    devs, table = _table(blobs, gpu)
+    ids = np.stack([rng.choice(n_exp, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    w = rng.random((n_tok, k)).astype(np.float32)
+    x = rng.standard_normal((n_tok, dm)).astype(np.float32)
+    want = np.zeros((n_tok, dm), np.float32)
+    bound = np.zeros((n_tok, dm), np.float64)
+    for t in range(n_tok):
+        res = [oracle.q4_0_qmm_forward_bounded(blobs[i], x[t], dm, dff) for i in ids[t]]
+        want[t] = oracle.combine_outputs(np.stack([r[0] for r in res]), w[t])
+        bound[t] = sum(float(w[t, i]) * res[i][1].astype(np.float64) for i in range(k))
+    got = mer.moe_forward(mer.WeightDtype.Q4_0, dm, dff, table, to_dev(ids, gpu), to_dev(w, gpu), to_dev(x, gpu),
+                          qmm=True).cpu().numpy()
+    torch.cuda.synchronize()
+    mer.take_device_status()
+    assert_qmm_close(got, want, bound, f"decode qmm variant GG={gg} GD={gd} paired={paired}")
     del devs
