@@ -207,3 +207,39 @@ def test_grouped_qmm_vs_oracle(mer, oracle, gpu):
     _closer_to_qmm(got, want, deq, "qmm grouped")
     mer.take_device_status()
     del devs
+
+
+@pytest.mark.parametrize("path", ["decode", "grouped"])
+def test_qmm_swiglu_limit_matches_oracle(mer, oracle, gpu, path):
+    """forward_qmm clamps the gate before SiLU as well (clamp_swiglu_gate,
+    inference.rs:4119); the limit binds on a good part of the rows."""
+    dm, dff = 512, 1024
+    say(f"qmm swiglu limit path={path}")
+    blobs = [make_expert(oracle, Q4, dm, dff, 90 + e) for e in range(3)]
+    devs, table = _table(blobs, gpu)
+    rng = np.random.default_rng(41)
+    n_tok, k = 3, 2
+    ids = np.stack([rng.choice(3, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    w = rng.random((n_tok, k)).astype(np.float32)
+    x = (rng.standard_normal((n_tok, dm)) * 3).astype(np.float32)
+    fn = mer.moe_grouped if path == "grouped" else mer.moe_forward
+    try:
+        mer.set_swiglu_limit(0.5)
+        oracle.set_swiglu_limit(0.5)
+        want = np.zeros((n_tok, dm), np.float32)
+        bound = np.zeros((n_tok, dm), np.float64)
+        for t in range(n_tok):
+            res = [oracle.q4_0_qmm_forward_bounded(blobs[i], x[t], dm, dff) for i in ids[t]]
+            want[t] = oracle.combine_outputs(np.stack([r[0] for r in res]), w[t])
+            bound[t] = sum(float(w[t, i]) * res[i][1].astype(np.float64) for i in range(k))
+        got = fn(mer.WeightDtype.Q4_0, dm, dff, table, to_dev(ids, gpu), to_dev(w, gpu), to_dev(x, gpu),
+                 qmm=True).cpu().numpy()
+    finally:
+        mer.set_swiglu_limit(None)
+        oracle.set_swiglu_limit(float("inf"))
+    assert_qmm_close(got, want, bound, f"qmm swiglu limit {path}")
+    unclamped = np.stack([oracle.combine_outputs(np.stack([oracle.q4_0_qmm_forward(blobs[i], x[t], dm, dff)
+                                                           for i in ids[t]]), w[t]) for t in range(n_tok)])
+    assert np.abs(unclamped - want).max() > 100 * np.abs(got - want).max()  # the clamp bound
+    mer.take_device_status()
+    del devs

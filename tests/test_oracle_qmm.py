@@ -120,7 +120,7 @@ def test_qmm_flip_bound_covers_a_real_flip(oracle):
 
 
 def test_qmm_rejects_unaligned_dimensions(oracle):
-    """q4_0_qmm_rejects_unaligned_dimensions (inference.rs:6597-...):
+    """q4_0_qmm_rejects_unaligned_dimensions (inference.rs:6597):
     InvalidLayout when d_model or d_ff is not a multiple of 32."""
     blob = np.zeros(oracle.expert_weight_bytes(Q4, 31, 32), np.uint8)
     with pytest.raises(ValueError, match="status 4"):
