@@ -178,3 +178,39 @@ def test_join_u32_does_not_sign_extend(tmp_path):
     assert r.returncode == 0, r.stderr[-2000:]
     out = subprocess.run([str(exe)], capture_output=True, text=True)
     assert out.returncode == 0 and out.stdout.strip() == "1234567880000001", out.stdout
+
+
+def test_header_is_plain_c_and_links_from_c(mer, tmp_path):
+    """include/mer_hip.h compiles as strict C99 and C++11, and a C program
+    links against libmer_hip.so and calls its host-only entry points (what a
+    cgo / FFI binding does): the byte size of a Mixtral Q4_0 expert, the
+    ABI version, and a refused call before mer_hip_init."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if not gcc:
+        pytest.skip("gcc not available")
+    inc = os.path.join(ROOT, "include")
+    libdir = os.path.dirname(mer._lib.LIB_PATH)
+    src = tmp_path / "use.c"
+    src.write_text(
+        '#include "mer_hip.h"\n'
+        "#include <stdio.h>\n"
+        "int main(void) {\n"
+        "  size_t n = mer_expert_weight_bytes(MER_DTYPE_Q4_0, 4096, 14336);\n"
+        "  int rc = mer_hip_expert_forward_qmm(NULL, 0, NULL, 0, 4096, 14336, NULL, 0, NULL);\n"
+        '  printf("%zu %d %d\\n", n, mer_hip_abi_version(), rc);\n'
+        "  return n == 99090432u && rc == MER_ERR_NOT_INITIALIZED ? 0 : 1;\n"
+        "}\n")
+    for std in (["-std=c99"], ["-x", "c++", "-std=c++11"]):
+        r = subprocess.run([gcc, *std, "-Wall", "-Wextra", "-pedantic", "-Werror", "-I", inc, "-c", str(src),
+                            "-o", str(tmp_path / "use.o")], capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr[-2000:]
+    exe = tmp_path / "use"
+    r = subprocess.run([gcc, "-std=c99", "-I", inc, str(src), "-o", str(exe), "-L", libdir, "-lmer_hip",
+                        f"-Wl,-rpath,{libdir}"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert out.stdout.split()[:2] == ["99090432", "1"]
