@@ -730,6 +730,26 @@ def main() -> int:
             "note": "the same steps as one mer_hip_moe_forward per layer (MER's call pattern), launched back to "
                     "back; avg_launch_us = HIP events around the pass / launches; frac counts the whole step by "
                     "the host clock, kernel_frac the average launch"}
+        if dtype == Q4 and not args.no_qmm_pass:
+            # the engine's default: one call per layer, Q4_0 through QMatMul
+            q_pl = [[a[:11] + (a[11] | 16,) + a[12:] for a in row] for row in pl_args]
+            torch.cuda.synchronize()
+            p0 = time.perf_counter()
+            ev_a.record()
+            for s in range(args.warmup, total_steps):
+                for a in q_pl[s]:
+                    rc = pl_fn(*a)
+                    if rc:
+                        mer.errors.raise_for_status(rc)
+            ev_b.record()
+            torch.cuda.synchronize()
+            p1 = time.perf_counter()
+            mer.take_device_status()
+            q_us = ev_a.elapsed_time(ev_b) * 1e3 / (args.steps * L)
+            result["per_layer"]["qmm"] = {
+                "value": args.steps / (p1 - p0) * cfg.get("tokens", 1), "ms_per_step": (p1 - p0) * 1e3 / args.steps,
+                "avg_launch_us": q_us, "kernel_frac": per_layer_bytes / (q_us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+                "note": "the same per-layer calls with MER_MOE_QMM (the engine's default Q4_0 arm)"}
     if dtype == Q4 and args.config in (0, 1) and not args.per_layer and not args.route_after_prev \
             and not args.no_qmm_pass:
         # The same steps with Candle's QMatMul arithmetic (MER_MOE_QMM): the
