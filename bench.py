@@ -315,22 +315,30 @@ def qmm_parity(dm, dff, step, blob_of, gpu_rows):
 
     threads = baseline_threads()
     rows, bounds, flagged = [], [], 0
+    blobs = {k: blob_of(k) for row in step for _, keys, _ in row for k in keys}  # fetched before the clock
+    n_experts = sum(len(keys) for row in step for _, keys, _ in row)
+    t0 = time.perf_counter()
     for row in step:
         acc = np.zeros(dm, np.float64)
         bnd = np.zeros(dm, np.float64)
         for x, keys, wts in row:
-            res = [mer_oracle.q4_0_qmm_forward_bounded(blob_of(k), x, dm, dff, nthreads=threads) for k in keys]
+            res = [mer_oracle.q4_0_qmm_forward_bounded(blobs[k], x, dm, dff, nthreads=threads) for k in keys]
             acc += mer_oracle.combine_outputs(np.stack([r[0] for r in res]), np.asarray(wts, np.float32)).astype(
                 np.float64)
             bnd += sum(abs(float(w)) * r[1].astype(np.float64) for w, r in zip(wts, res))
             flagged += sum(r[2] for r in res)
         rows.append(acc)
         bounds.append(bnd)
+    spent = time.perf_counter() - t0
     ref = np.stack(rows)
     got = np.asarray(gpu_rows, np.float64).reshape(ref.shape)
     bar = 1e-3 * np.abs(ref) + 1e-3 * max(1.0, 1e-3 * float(np.abs(ref).max()))
     err = np.abs(ref - got)
-    return {"parity_worst_ratio": float((err / (bar + np.stack(bounds))).max()),
+    return {"cpu_ms_per_expert": spent / max(n_experts, 1) * 1e3, "cpu_threads": threads,
+            "cpu_note": "the oracle's scalar-C restatement of the QMatMul arithmetic on the same step, flip bound "
+                        "included (Candle's own AVX kernels are faster; ~27 ms per Mixtral expert in the "
+                        "reference's notes, 16 cores)",
+            "parity_worst_ratio": float((err / (bar + np.stack(bounds))).max()),
             "rows_beyond_ffn_bar": int((err > bar).sum()), "h_elements_flagged": int(flagged),
             "parity_bar": "1e-3 |ref| + 1e-3 max(1, 1e-3 max|ref|) + the oracle's flip bound (h elements within "
                           "1e-3 steps of a Q8_0 rounding midpoint may round either way in another f32 order)"}
