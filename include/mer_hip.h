@@ -212,7 +212,9 @@ int mer_hip_expert_forward(int dtype, const void *d_bytes, size_t len,
  * run_inference_q4_0_qmm / forward_q4_0_qmm_from_exact_bytes
  * (inference.rs:4159-4243) on VRAM-resident Q4_0 bytes, with the arithmetic
  * of MER_MOE_QMM.  Same validation and errors as mer_hip_expert_forward
- * plus MER_ERR_INVALID_LAYOUT for dims that are not multiples of 64. */
+ * plus MER_ERR_INVALID_LAYOUT for dims that are not multiples of 64 and
+ * MER_ERR_MISALIGNED for expert bytes that are not 4-byte aligned (the
+ * 22-bit entry point runs those on its flat-layout kernel instead). */
 int mer_hip_expert_forward_qmm(const void *d_bytes, size_t len, const float *d_x, size_t x_len, size_t d_model,
                                size_t d_ff, float *d_y, size_t y_len, void *stream);
 
